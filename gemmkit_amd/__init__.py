@@ -1,0 +1,481 @@
+"""gemmkit_amd -- gemmkit's GEMM API on MI355X (gfx950) matrix cores.
+
+Python mirror of the reference's Rust surface (gemmkit/src/lib.rs:98-148),
+calling the hand-written HIP kernels of ``libgemmkit_hip.so`` through its C ABI
+(``include/gemmkit_hip.h``).  Names, argument order and meaning follow the
+reference:
+
+===============================  ==============================================
+reference (gemmkit/src/...)      here
+===============================  ==============================================
+``MatRef`` / ``MatMut``          :class:`MatRef` / :class:`MatMut` over a 1-D
+  (api.rs:92-180)                device tensor (the "slice"), strides in elements
+``gemm``, ``gemm_with``          :func:`gemm` (f32, bf16), ``ws=`` for ``_with``
+``gemm_unchecked(_with)``        :func:`gemm_unchecked`
+``gemm_i8(_with)``               :func:`gemm_i8`
+``gemm_i8_unchecked(_with)``     :func:`gemm_i8_unchecked`
+``gemm_i8_requant(_u8)``         :func:`gemm_i8_requant`, :func:`gemm_i8_requant_u8`
+``..._requant_unchecked``        :func:`gemm_i8_requant_unchecked`
+``prepack_rhs_i8``               :func:`prepack_rhs_i8` -> :class:`PackedRhs`
+``gemm_i8_packed_b(_with)``      :func:`gemm_i8_packed_b`
+``gemm_batched(_with)``          :func:`gemm_batched`
+``Parallelism``                  :class:`Parallelism` (accepted, ignored: the
+                                 device grid decides)
+``Workspace``                    :class:`Workspace` (a device scratch arena)
+===============================  ==============================================
+
+Where the reference panics, these functions raise :class:`GemmkitError` with
+the reference's message.  Extensions of this engine (no reference
+counterpart): f32 output for bf16 GEMMs (:func:`gemm_bf16_f32out`,
+:func:`gemm_batched_bf16_f32out`), per-column requant vectors
+(``RequantScale.PerCol``, ``Requantize(bias_axis="col")``), a ReLU after
+requantization (``Requantize(relu=True)``), and prepacked-B requantization
+(:func:`gemm_i8_packed_b_requant`).
+
+All tensors must live on the HIP device; calls are synchronous by default and
+run on torch's current stream.  There is no CPU fallback: a missing library
+raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import Optional, Sequence, Union
+
+import torch
+
+from . import _lib
+from ._lib import MatMutC, MatRefC, RequantizeC
+
+__all__ = [
+    "GemmkitError", "MatRef", "MatMut", "Parallelism", "Workspace", "RequantScale",
+    "Requantize", "PackedRhs", "gemm", "gemm_unchecked", "gemm_bf16_f32out", "gemm_i8",
+    "gemm_i8_unchecked", "gemm_i8_requant", "gemm_i8_requant_u8", "gemm_i8_requant_unchecked",
+    "gemm_i8_requant_u8_unchecked", "prepack_rhs_i8", "gemm_i8_packed_b",
+    "gemm_i8_packed_b_unchecked", "gemm_i8_packed_b_requant", "gemm_i8_packed_b_requant_u8",
+    "gemm_batched", "gemm_batched_unchecked", "gemm_batched_bf16_f32out", "set_synchronous",
+    "library_path", "version",
+]
+
+library_path = _lib.LIB_PATH
+
+
+class GemmkitError(RuntimeError):
+    """Raised where the reference panics; ``code`` is the C ABI's gk_status."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(message)
+        self.code = code
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise GemmkitError(rc, _lib.last_error())
+
+
+def version() -> str:
+    return _lib.lib().gk_version().decode()
+
+
+def set_synchronous(on: bool) -> None:
+    """True (default): every call waits for its kernels, like the reference."""
+    _lib.lib().gk_set_synchronous(1 if on else 0)
+
+
+def _bind_stream() -> None:
+    L = _lib.lib()
+    s = torch.cuda.current_stream().cuda_stream
+    L.gk_set_stream(C.c_void_p(s))
+
+
+# ---------------------------------------------------------------------- types
+
+class Parallelism:
+    """Parallelism (src/parallel.rs:25): ``Serial`` or ``Rayon(n)`` (0 = all)."""
+
+    def __init__(self, threads: int):
+        self.threads = int(threads)
+
+    @staticmethod
+    def Rayon(n: int) -> "Parallelism":  # noqa: N802 -- mirrors the Rust variant
+        return Parallelism(n)
+
+    def __repr__(self) -> str:
+        return "Serial" if self.threads == 1 else f"Rayon({self.threads})"
+
+
+Parallelism.Serial = Parallelism(1)  # type: ignore[attr-defined]
+
+
+def _par(par: Optional[Parallelism]) -> int:
+    return 1 if par is None else par.threads
+
+
+class Workspace:
+    """Workspace (src/workspace.rs:53): a device scratch arena owned by the caller."""
+
+    def __init__(self) -> None:
+        self._h = _lib.lib().gk_workspace_new()
+
+    @property
+    def handle(self):
+        return self._h
+
+    def bytes(self) -> int:
+        return int(_lib.lib().gk_workspace_bytes(self._h))
+
+    def __del__(self) -> None:
+        h, self._h = getattr(self, "_h", None), None
+        if h:
+            _lib.lib().gk_workspace_free(h)
+
+
+def _ws(ws: Optional[Workspace]):
+    return None if ws is None else ws.handle
+
+
+def _slice(data: torch.Tensor, what: str) -> torch.Tensor:
+    if not isinstance(data, torch.Tensor):
+        raise TypeError(f"gemmkit_amd: {what} data must be a torch.Tensor")
+    if data.device.type != "cuda":
+        raise GemmkitError(-7, f"gemmkit_amd: {what} data must live on the HIP device")
+    if not data.is_contiguous():
+        raise TypeError(f"gemmkit_amd: {what} data must be a contiguous slice")
+    return data
+
+
+class MatRef:
+    """Immutable strided view (src/api.rs:92-140): element (i, j) at ``i*rs + j*cs``."""
+
+    def __init__(self, data: torch.Tensor, rows: int, cols: int, rs: int, cs: int):
+        self.data, self.rows, self.cols, self.rs, self.cs = data, int(rows), int(cols), int(rs), int(cs)
+
+    @classmethod
+    def from_row_major(cls, data, rows, cols):
+        return cls(data, rows, cols, cols, 1)
+
+    @classmethod
+    def from_col_major(cls, data, rows, cols):
+        return cls(data, rows, cols, 1, rows)
+
+    def _c(self, dtype: torch.dtype, what: str) -> MatRefC:
+        d = _slice(self.data, what)
+        if d.dtype != dtype:
+            raise TypeError(f"gemmkit_amd: {what} must be {dtype}, got {d.dtype}")
+        return MatRefC(d.data_ptr(), d.numel(), self.rows, self.cols, self.rs, self.cs)
+
+
+class MatMut(MatRef):
+    """Mutable strided view (src/api.rs:107-180); the output C."""
+
+    def _c(self, dtype: torch.dtype, what: str) -> MatMutC:  # type: ignore[override]
+        d = _slice(self.data, what)
+        if d.dtype != dtype:
+            raise TypeError(f"gemmkit_amd: {what} must be {dtype}, got {d.dtype}")
+        return MatMutC(d.data_ptr(), d.numel(), self.rows, self.cols, self.rs, self.cs)
+
+
+def _bf16_bits(x: float) -> int:
+    """f32 -> bf16 bit pattern, round to nearest even (NaN quieted)."""
+    return int(torch.tensor([x], dtype=torch.float32).to(torch.bfloat16).view(torch.int16)
+               .item()) & 0xFFFF
+
+
+# ------------------------------------------------------------------ plain gemm
+
+def gemm(alpha, a: MatRef, b: MatRef, beta, c: MatMut,
+         par: Optional[Parallelism] = None, ws: Optional[Workspace] = None) -> None:
+    """``gemm`` / ``gemm_with`` (src/api.rs:400-450): C <- alpha*A*B + beta*C.
+
+    The element type follows the tensors: float32 or bfloat16 (f32 accumulation,
+    one RNE narrowing; ``alpha``/``beta`` are rounded to bf16 like the
+    reference's bf16 scalars)."""
+    _bind_stream()
+    L = _lib.lib()
+    dt = a.data.dtype
+    if dt == torch.float32:
+        _check(L.gk_gemm_f32(_ws(ws), float(alpha), a._c(dt, "A"), b._c(dt, "B"), float(beta),
+                             c._c(dt, "C"), _par(par)))
+    elif dt == torch.bfloat16:
+        _check(L.gk_gemm_bf16(_ws(ws), _bf16_bits(alpha), a._c(dt, "A"), b._c(dt, "B"),
+                              _bf16_bits(beta), c._c(dt, "C"), _par(par)))
+    else:
+        raise TypeError(f"gemmkit_amd: gemm supports float32 and bfloat16, got {dt}")
+
+
+def gemm_bf16_f32out(alpha: float, a: MatRef, b: MatRef, beta: float, c: MatMut,
+                     par: Optional[Parallelism] = None, ws: Optional[Workspace] = None) -> None:
+    """Extension: bf16 inputs, f32 accumulation, f32 alpha/beta and output."""
+    _bind_stream()
+    _check(_lib.lib().gk_gemm_bf16_f32out(_ws(ws), float(alpha), a._c(torch.bfloat16, "A"),
+                                          b._c(torch.bfloat16, "B"), float(beta),
+                                          c._c(torch.float32, "C"), _par(par)))
+
+
+def _ptr(t: Optional[torch.Tensor], off: int = 0) -> Optional[int]:
+    if t is None:
+        return None
+    return t.data_ptr() + off * t.element_size()
+
+
+def gemm_unchecked(m, k, n, alpha, a: torch.Tensor, rsa, csa, b: torch.Tensor, rsb, csb, beta,
+                   c: torch.Tensor, rsc, csc, par=None, ws=None, a_off=0, b_off=0, c_off=0):
+    """``gemm_unchecked(_with)`` (src/api.rs:469-580): raw strides, no checks.
+
+    ``*_off`` are element offsets of the base pointers (negative strides walk
+    backwards from there, as the reference allows on this tier)."""
+    _bind_stream()
+    L = _lib.lib()
+    if a.dtype == torch.float32:
+        _check(L.gk_gemm_f32_unchecked(_ws(ws), m, k, n, float(alpha), _ptr(a, a_off), rsa, csa,
+                                       _ptr(b, b_off), rsb, csb, float(beta), _ptr(c, c_off), rsc,
+                                       csc, _par(par)))
+    elif a.dtype == torch.bfloat16:
+        _check(L.gk_gemm_bf16_unchecked(_ws(ws), m, k, n, _bf16_bits(alpha), _ptr(a, a_off), rsa,
+                                        csa, _ptr(b, b_off), rsb, csb, _bf16_bits(beta),
+                                        _ptr(c, c_off), rsc, csc, _par(par)))
+    else:
+        raise TypeError(f"gemmkit_amd: gemm_unchecked supports float32 and bfloat16, got {a.dtype}")
+
+
+# -------------------------------------------------------------------- i8 gemm
+
+def gemm_i8(alpha: int, a: MatRef, b: MatRef, beta: int, c: MatMut,
+            par: Optional[Parallelism] = None, ws: Optional[Workspace] = None) -> None:
+    """``gemm_i8`` / ``gemm_i8_with`` (src/api/int8.rs:22-73): wrapping i32."""
+    _bind_stream()
+    _check(_lib.lib().gk_gemm_i8(_ws(ws), int(alpha), a._c(torch.int8, "A"),
+                                 b._c(torch.int8, "B"), int(beta), c._c(torch.int32, "C"),
+                                 _par(par)))
+
+
+def gemm_i8_unchecked(m, k, n, alpha, a, rsa, csa, b, rsb, csb, beta, c, rsc, csc, par=None,
+                      ws=None, a_off=0, b_off=0, c_off=0) -> None:
+    """``gemm_i8_unchecked(_with)`` (src/api/int8.rs:86-178)."""
+    _bind_stream()
+    _check(_lib.lib().gk_gemm_i8_unchecked(_ws(ws), m, k, n, int(alpha), _ptr(a, a_off), rsa,
+                                           csa, _ptr(b, b_off), rsb, csb, int(beta),
+                                           _ptr(c, c_off), rsc, csc, _par(par)))
+
+
+# ------------------------------------------------------------------- requant
+
+class RequantScale:
+    """RequantScale (src/api/int8.rs:185-194): ``PerTensor(f)`` or ``PerRow(tensor)``;
+    ``PerCol(tensor)`` is this engine's per-output-column extension."""
+
+    def __init__(self, kind: str, value):
+        self.kind, self.value = kind, value
+
+    @staticmethod
+    def PerTensor(s: float) -> "RequantScale":  # noqa: N802
+        return RequantScale("tensor", float(s))
+
+    @staticmethod
+    def PerRow(s: torch.Tensor) -> "RequantScale":  # noqa: N802
+        return RequantScale("row", s)
+
+    @staticmethod
+    def PerCol(s: torch.Tensor) -> "RequantScale":  # noqa: N802
+        return RequantScale("col", s)
+
+
+@dataclass
+class Requantize:
+    """Requantize (src/api/int8.rs:196-209).  ``bias`` is per row like the
+    reference unless ``bias_axis="col"``; a per-column scale implies a per-column
+    bias.  ``relu`` (extension) clamps the output below at the zero point."""
+    scale: RequantScale
+    zero_point: int = 0
+    bias: Optional[torch.Tensor] = None
+    bias_axis: str = "row"
+    relu: bool = False
+
+    def _c(self) -> RequantizeC:
+        # One channel axis serves scales and bias, as the reference's bias_dim
+        # does (src/dispatch/int.rs:640-660).
+        if self.scale.kind == "row" and self.bias is not None and self.bias_axis == "col":
+            raise GemmkitError(-4, "gemmkit_amd: per-row scales need a per-row bias")
+        axis = 1 if (self.scale.kind == "col" or self.bias_axis == "col") else 0
+        r = RequantizeC()
+        if self.scale.kind == "tensor":
+            r.scale, r.scales, r.scales_len = self.scale.value, None, 0
+        else:
+            s = _slice(self.scale.value, "requantize scales")
+            if s.dtype != torch.float32:
+                raise TypeError("gemmkit_amd: requantize scales must be float32")
+            r.scale, r.scales, r.scales_len = 0.0, s.data_ptr(), s.numel()
+        r.zero_point = int(self.zero_point)
+        if self.bias is not None:
+            bt = _slice(self.bias, "requantize bias")
+            if bt.dtype != torch.int32:
+                raise TypeError("gemmkit_amd: requantize bias must be int32")
+            r.bias, r.bias_len = bt.data_ptr(), bt.numel()
+        else:
+            r.bias, r.bias_len = None, 0
+        r.axis = axis
+        r.act = 1 if self.relu else 0
+        return r
+
+
+def gemm_i8_requant(a: MatRef, b: MatRef, req: Requantize, c: MatMut,
+                    par: Optional[Parallelism] = None, ws: Optional[Workspace] = None) -> None:
+    """``gemm_i8_requant(_with)`` (src/api/int8.rs:230-328): i8 out, [-128, 127]."""
+    _bind_stream()
+    _check(_lib.lib().gk_gemm_i8_requant(_ws(ws), a._c(torch.int8, "A"), b._c(torch.int8, "B"),
+                                         C.byref(req._c()), c._c(torch.int8, "C"), _par(par)))
+
+
+def gemm_i8_requant_u8(a: MatRef, b: MatRef, req: Requantize, c: MatMut,
+                       par: Optional[Parallelism] = None, ws: Optional[Workspace] = None) -> None:
+    """``gemm_i8_requant_u8(_with)`` (src/api/int8.rs:479-555): u8 out, [0, 255]."""
+    _bind_stream()
+    _check(_lib.lib().gk_gemm_i8_requant_u8(_ws(ws), a._c(torch.int8, "A"),
+                                            b._c(torch.int8, "B"), C.byref(req._c()),
+                                            c._c(torch.uint8, "C"), _par(par)))
+
+
+def gemm_i8_requant_unchecked(m, k, n, a, rsa, csa, b, rsb, csb, scale, row_scales, zero_point,
+                              bias, c, rsc, csc, par=None, ws=None, axis=0, relu=False,
+                              a_off=0, b_off=0, c_off=0) -> None:
+    """``gemm_i8_requant_unchecked(_with)`` (src/api/int8.rs:347-457)."""
+    _bind_stream()
+    _check(_lib.lib().gk_gemm_i8_requant_unchecked(
+        _ws(ws), m, k, n, _ptr(a, a_off), rsa, csa, _ptr(b, b_off), rsb, csb, float(scale),
+        _ptr(row_scales), 1 if row_scales is not None else 0, int(zero_point), _ptr(bias),
+        1 if bias is not None else 0, _ptr(c, c_off), rsc, csc, _par(par), int(axis),
+        1 if relu else 0))
+
+
+def gemm_i8_requant_u8_unchecked(m, k, n, a, rsa, csa, b, rsb, csb, scale, row_scales,
+                                 zero_point, bias, c, rsc, csc, par=None, ws=None, axis=0,
+                                 relu=False, a_off=0, b_off=0, c_off=0) -> None:
+    """``gemm_i8_requant_u8_unchecked(_with)`` (src/api/int8.rs:562-672)."""
+    _bind_stream()
+    _check(_lib.lib().gk_gemm_i8_requant_u8_unchecked(
+        _ws(ws), m, k, n, _ptr(a, a_off), rsa, csa, _ptr(b, b_off), rsb, csb, float(scale),
+        _ptr(row_scales), 1 if row_scales is not None else 0, int(zero_point), _ptr(bias),
+        1 if bias is not None else 0, _ptr(c, c_off), rsc, csc, _par(par), int(axis),
+        1 if relu else 0))
+
+
+# ---------------------------------------------------------------- prepacked B
+
+class PackedRhs:
+    """PackedRhs<i8> (src/api/packed.rs:34-52): B packed once on the device."""
+
+    def __init__(self, handle):
+        self._h = handle
+
+    @property
+    def handle(self):
+        return self._h
+
+    def rows(self) -> int:
+        return int(_lib.lib().gk_packed_rhs_rows(self._h))
+
+    def cols(self) -> int:
+        return int(_lib.lib().gk_packed_rhs_cols(self._h))
+
+    def __del__(self) -> None:
+        h, self._h = getattr(self, "_h", None), None
+        if h:
+            _lib.lib().gk_packed_rhs_free(h)
+
+
+def prepack_rhs_i8(b: MatRef) -> PackedRhs:
+    """``prepack_rhs_i8`` (src/api/packed.rs:372-386)."""
+    _bind_stream()
+    out = C.c_void_p()
+    _check(_lib.lib().gk_prepack_rhs_i8(b._c(torch.int8, "B"), C.byref(out)))
+    return PackedRhs(out.value)
+
+
+def gemm_i8_packed_b(alpha: int, a: MatRef, packed: PackedRhs, beta: int, c: MatMut,
+                     par: Optional[Parallelism] = None, ws: Optional[Workspace] = None) -> None:
+    """``gemm_i8_packed_b(_with)`` (src/api/packed.rs:473-560): requires a
+    column-major-ish C, like the reference."""
+    _bind_stream()
+    _check(_lib.lib().gk_gemm_i8_packed_b(_ws(ws), int(alpha), a._c(torch.int8, "A"),
+                                          packed.handle, int(beta), c._c(torch.int32, "C"),
+                                          _par(par)))
+
+
+def gemm_i8_packed_b_unchecked(alpha, m, a, rsa, csa, packed: PackedRhs, beta, c, rsc, csc,
+                               par=None, ws=None, a_off=0, c_off=0) -> None:
+    """``gemm_i8_packed_b_unchecked(_with)`` (src/api/packed.rs:575-656)."""
+    _bind_stream()
+    _check(_lib.lib().gk_gemm_i8_packed_b_unchecked(_ws(ws), int(alpha), m, _ptr(a, a_off), rsa,
+                                                    csa, packed.handle, int(beta),
+                                                    _ptr(c, c_off), rsc, csc, _par(par)))
+
+
+def gemm_i8_packed_b_requant(a: MatRef, packed: PackedRhs, req: Requantize, c: MatMut,
+                             par: Optional[Parallelism] = None,
+                             ws: Optional[Workspace] = None) -> None:
+    """Extension: requantizing GEMM against a prepacked B (i8 out, any C layout)."""
+    _bind_stream()
+    _check(_lib.lib().gk_gemm_i8_packed_b_requant(_ws(ws), a._c(torch.int8, "A"), packed.handle,
+                                                  C.byref(req._c()), c._c(torch.int8, "C"),
+                                                  _par(par)))
+
+
+def gemm_i8_packed_b_requant_u8(a: MatRef, packed: PackedRhs, req: Requantize, c: MatMut,
+                                par: Optional[Parallelism] = None,
+                                ws: Optional[Workspace] = None) -> None:
+    """Extension: the u8-output twin of :func:`gemm_i8_packed_b_requant`."""
+    _bind_stream()
+    _check(_lib.lib().gk_gemm_i8_packed_b_requant_u8(_ws(ws), a._c(torch.int8, "A"),
+                                                     packed.handle, C.byref(req._c()),
+                                                     c._c(torch.uint8, "C"), _par(par)))
+
+
+# ------------------------------------------------------------------- batched
+
+def gemm_batched(batch: int, alpha, a: MatRef, a_batch_stride: int, b: MatRef,
+                 b_batch_stride: int, beta, c: MatMut, c_batch_stride: int,
+                 par: Optional[Parallelism] = None, ws: Optional[Workspace] = None) -> None:
+    """``gemm_batched(_with)`` (src/api/batched.rs:188-283), float32 or bfloat16."""
+    _bind_stream()
+    L = _lib.lib()
+    dt = a.data.dtype
+    if dt == torch.float32:
+        _check(L.gk_gemm_batched_f32(_ws(ws), batch, float(alpha), a._c(dt, "A"), a_batch_stride,
+                                     b._c(dt, "B"), b_batch_stride, float(beta), c._c(dt, "C"),
+                                     c_batch_stride, _par(par)))
+    elif dt == torch.bfloat16:
+        _check(L.gk_gemm_batched_bf16(_ws(ws), batch, _bf16_bits(alpha), a._c(dt, "A"),
+                                      a_batch_stride, b._c(dt, "B"), b_batch_stride,
+                                      _bf16_bits(beta), c._c(dt, "C"), c_batch_stride, _par(par)))
+    else:
+        raise TypeError(f"gemmkit_amd: gemm_batched supports float32 and bfloat16, got {dt}")
+
+
+def gemm_batched_unchecked(batch, m, k, n, alpha, a, rsa, csa, a_bs, b, rsb, csb, b_bs, beta,
+                           c, rsc, csc, c_bs, par=None, ws=None) -> None:
+    """``gemm_batched_unchecked(_with)`` (src/api/batched.rs:594-700)."""
+    _bind_stream()
+    L = _lib.lib()
+    if a.dtype == torch.float32:
+        _check(L.gk_gemm_batched_f32_unchecked(_ws(ws), batch, m, k, n, float(alpha), _ptr(a),
+                                               rsa, csa, a_bs, _ptr(b), rsb, csb, b_bs,
+                                               float(beta), _ptr(c), rsc, csc, c_bs, _par(par)))
+    elif a.dtype == torch.bfloat16:
+        _check(L.gk_gemm_batched_bf16_unchecked(_ws(ws), batch, m, k, n, _bf16_bits(alpha),
+                                                _ptr(a), rsa, csa, a_bs, _ptr(b), rsb, csb, b_bs,
+                                                _bf16_bits(beta), _ptr(c), rsc, csc, c_bs,
+                                                _par(par)))
+    else:
+        raise TypeError("gemmkit_amd: gemm_batched_unchecked supports float32 and bfloat16")
+
+
+def gemm_batched_bf16_f32out(batch: int, alpha: float, a: MatRef, a_batch_stride: int,
+                             b: MatRef, b_batch_stride: int, beta: float, c: MatMut,
+                             c_batch_stride: int, par: Optional[Parallelism] = None,
+                             ws: Optional[Workspace] = None) -> None:
+    """Extension: batched bf16 x bf16 -> f32 (attention-score shape)."""
+    _bind_stream()
+    _check(_lib.lib().gk_gemm_batched_bf16_f32out(
+        _ws(ws), batch, float(alpha), a._c(torch.bfloat16, "A"), a_batch_stride,
+        b._c(torch.bfloat16, "B"), b_batch_stride, float(beta), c._c(torch.float32, "C"),
+        c_batch_stride, _par(par)))

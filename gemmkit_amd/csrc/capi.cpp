@@ -1,0 +1,1012 @@
+// capi.cpp -- the C ABI of include/gemmkit_hip.h: validation, degenerate cases,
+// orientation, route choice and launches.
+//
+// Layering follows gemmkit's own (ARCHITECTURE.md "The Layer Stack"):
+//   checked entries  -> validate_gemm_views and friends (src/api.rs:188-314,
+//                       src/adapter.rs:130-273, src/api/batched.rs:31-163),
+//                       same conditions, same "gemmkit: ..." wording;
+//   unchecked entries-> straight to the dispatch layer (src/api.rs:469-580);
+//   dispatch         -> m|n == 0 returns, k == 0 / alpha == 0 scales C
+//                       (src/dispatch.rs:345-358, src/dispatch/int.rs:131-163),
+//                       orientation swap (src/dispatch.rs:395-417), then the
+//                       GEMV route for skinny products or the MFMA tile grid.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "../../include/gemmkit_hip.h"
+#include "internal.h"
+
+using namespace gk;
+
+// ------------------------------------------------------------------ state
+
+namespace {
+
+thread_local std::string tl_error;
+thread_local hipStream_t tl_stream = nullptr;
+thread_local int tl_sync = 1;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    tl_error = buf;
+    return code;
+}
+
+int ok() {
+    tl_error.clear();
+    return GK_OK;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(GK_ERR_DEVICE, "gemmkit: HIP error in %s: %s", what, hipGetErrorString(e));
+}
+
+std::once_flag g_init_once;
+int g_init_status = GK_OK;
+std::string g_init_error;
+int g_num_cus = 256;
+
+int device_init() {
+    std::call_once(g_init_once, [] {
+        int n = 0;
+        hipError_t e = hipGetDeviceCount(&n);
+        if (e != hipSuccess || n == 0) {
+            g_init_status = GK_ERR_DEVICE;
+            g_init_error = std::string("gemmkit: no HIP device available (") +
+                           hipGetErrorString(e) + ")";
+            return;
+        }
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, dev) == hipSuccess && prop.multiProcessorCount > 0)
+            g_num_cus = prop.multiProcessorCount;
+    });
+    if (g_init_status != GK_OK) return fail(g_init_status, "%s", g_init_error.c_str());
+    return GK_OK;
+}
+
+// ---------------------------------------------------------- Rust formatting
+
+// Rust's `{}` for f32: the shortest decimal that reads back as the same f32,
+// written positionally (no exponent).  Used to reproduce the reference's
+// "requantize scale ({s}) must be finite and > 0" message.
+std::string rust_f32(float x) {
+    if (std::isnan(x)) return "NaN";
+    if (std::isinf(x)) return x > 0 ? "inf" : "-inf";
+    if (x == 0.0f) return std::signbit(x) ? "-0" : "0";
+    char buf[64];
+    int prec = 1;
+    for (; prec <= 9; ++prec) {
+        snprintf(buf, sizeof buf, "%.*e", prec - 1, (double)x);
+        if ((float)strtod(buf, nullptr) == x) break;
+    }
+    // buf = [-]d.ddde[+-]XX
+    std::string s(buf);
+    bool neg = s[0] == '-';
+    if (neg) s = s.substr(1);
+    size_t epos = s.find('e');
+    int exp10 = atoi(s.c_str() + epos + 1);
+    std::string digits;
+    for (size_t i = 0; i < epos; ++i)
+        if (s[i] != '.') digits += s[i];
+    while (digits.size() > 1 && digits.back() == '0') digits.pop_back();
+    // value = 0.d1d2d3... * 10^(exp10+1)
+    int point = exp10 + 1;
+    std::string out;
+    if (point <= 0) {
+        out = "0." + std::string(-point, '0') + digits;
+    } else if ((size_t)point >= digits.size()) {
+        out = digits + std::string(point - digits.size(), '0');
+    } else {
+        out = digits.substr(0, point) + "." + digits.substr(point);
+    }
+    return neg ? "-" + out : out;
+}
+
+// ----------------------------------------------------------- view checks
+
+// extent (src/api.rs:188-215): one past the highest element offset, or -1
+// when a stride paired with a dimension > 1 is negative or arithmetic
+// overflows.
+bool extent(size_t rows, size_t cols, ptrdiff_t rs, ptrdiff_t cs, size_t *out) {
+    if (rows == 0 || cols == 0) {
+        *out = 0;
+        return true;
+    }
+    __int128 lo = 0, hi = 0;
+    const size_t dims[2] = {rows, cols};
+    const ptrdiff_t strides[2] = {rs, cs};
+    for (int t = 0; t < 2; ++t) {
+        if (dims[t] > (size_t)PTRDIFF_MAX) return false;
+        __int128 e = (__int128)(ptrdiff_t)(dims[t] - 1) * strides[t];
+        if (e > PTRDIFF_MAX || e < PTRDIFF_MIN) return false;
+        if (e < 0) lo += e; else hi += e;
+        if (hi > PTRDIFF_MAX || lo < PTRDIFF_MIN) return false;
+    }
+    if (lo < 0) return false;
+    if (hi + 1 > (__int128)SIZE_MAX) return false;
+    *out = (size_t)hi + 1;
+    return true;
+}
+
+// check_view (src/api.rs:197-213).
+int check_view(size_t len, size_t rows, size_t cols, ptrdiff_t rs, ptrdiff_t cs,
+               const char *name, const char *unchecked_name = "gemm_unchecked") {
+    size_t need = 0;
+    if (!extent(rows, cols, rs, cs, &need))
+        return fail(GK_ERR_VIEW,
+                    "gemmkit: %s view has negative strides or is too large to address; use %s",
+                    name, unchecked_name);
+    if (need > len)
+        return fail(GK_ERR_VIEW,
+                    "gemmkit: %s view of %zux%zu (strides %td,%td) needs %zu elements but slice "
+                    "has %zu",
+                    name, rows, cols, rs, cs, need, len);
+    return GK_OK;
+}
+
+// self_aliases (src/api.rs:236-250).
+bool self_aliases(size_t rows, size_t cols, ptrdiff_t rs, ptrdiff_t cs) {
+    if (rows == 0 || cols == 0) return false;
+    bool hr = rows > 1, hc = cols > 1;
+    size_t ars = (size_t)(rs < 0 ? -(__int128)rs : rs), acs = (size_t)(cs < 0 ? -(__int128)cs : cs);
+    if (!hr && !hc) return false;
+    if (hr && !hc) return ars == 0;
+    if (!hr && hc) return acs == 0;
+    size_t sm_s, sm_d, big;
+    if (ars <= acs) { sm_s = ars; sm_d = rows; big = acs; } else { sm_s = acs; sm_d = cols; big = ars; }
+    __int128 span = (__int128)sm_s * sm_d;
+    return sm_s == 0 || (__int128)big < span;
+}
+
+// overlaps_bytes (src/api.rs:520-536).
+bool overlaps_bytes(const void *pa, size_t na, size_t sa, const void *pb, size_t nb, size_t sb) {
+    uintptr_t a0 = (uintptr_t)pa, a1 = a0 + na * sa;
+    uintptr_t b0 = (uintptr_t)pb, b1 = b0 + nb * sb;
+    return a0 < b1 && b0 < a1;
+}
+
+// validate_gemm_views (src/api.rs:270-314).
+int validate_gemm_views(const gk_mat_ref *a, const gk_mat_ref *b, const gk_mat_mut *c,
+                        size_t si, size_t so) {
+    if (!a || !b || !c) return fail(GK_ERR_ARG, "gemmkit: null view argument");
+    if (a->cols != b->rows)
+        return fail(GK_ERR_SHAPE, "gemmkit: A.cols (%zu) != B.rows (%zu)", a->cols, b->rows);
+    if (a->rows != c->rows)
+        return fail(GK_ERR_SHAPE, "gemmkit: A.rows (%zu) != C.rows (%zu)", a->rows, c->rows);
+    if (b->cols != c->cols)
+        return fail(GK_ERR_SHAPE, "gemmkit: B.cols (%zu) != C.cols (%zu)", b->cols, c->cols);
+    int r;
+    if ((r = check_view(a->len, a->rows, a->cols, a->rs, a->cs, "A"))) return r;
+    if ((r = check_view(b->len, b->rows, b->cols, b->rs, b->cs, "B"))) return r;
+    if ((r = check_view(c->len, c->rows, c->cols, c->rs, c->cs, "C"))) return r;
+    if (self_aliases(c->rows, c->cols, c->rs, c->cs))
+        return fail(GK_ERR_ALIAS,
+                    "gemmkit: C view aliases itself (strides %td,%td map distinct elements to the "
+                    "same memory); C must address each (i,j) uniquely",
+                    c->rs, c->cs);
+    if (overlaps_bytes(c->data, c->len, so, a->data, a->len, si) ||
+        overlaps_bytes(c->data, c->len, so, b->data, b->len, si))
+        return fail(GK_ERR_ALIAS, "gemmkit: C aliases A or B");
+    return GK_OK;
+}
+
+// ------------------------------------------------------------ workspace
+
+}  // namespace
+
+struct gk_workspace {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+};
+
+struct gk_packed_rhs {
+    int8_t *buf = nullptr;  // n x ld, k-contiguous rows (B transposed), zero padded
+    size_t k = 0, n = 0;
+    int64_t ld = 0;
+};
+
+namespace {
+
+thread_local gk_workspace *tl_ws = nullptr;
+
+gk_workspace *resolve_ws(gk_workspace *ws) {
+    if (ws) return ws;
+    if (!tl_ws) tl_ws = new gk_workspace();
+    return tl_ws;
+}
+
+// Returns a device region of at least `bytes`, growing the arena when needed.
+int ws_reserve(gk_workspace *ws, size_t bytes, void **out) {
+    if (ws->bytes < bytes) {
+        size_t want = std::max(bytes, ws->bytes + ws->bytes / 2);
+        want = (want + 0xFFFFF) & ~(size_t)0xFFFFF;
+        if (ws->ptr) {
+            // Work already queued may still read the old arena.
+            hipError_t e = hipDeviceSynchronize();
+            if (e != hipSuccess) return hip_fail(e, "workspace grow");
+            (void)hipFree(ws->ptr);
+            ws->ptr = nullptr;
+            ws->bytes = 0;
+        }
+        hipError_t e = hipMalloc(&ws->ptr, want);
+        if (e != hipSuccess) {
+            ws->ptr = nullptr;
+            return fail(GK_ERR_NOMEM, "gemmkit: workspace allocation of %zu bytes failed", want);
+        }
+        ws->bytes = want;
+    }
+    *out = ws->ptr;
+    return GK_OK;
+}
+
+int finish(const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, what);
+    if (tl_sync) {
+        e = hipStreamSynchronize(tl_stream);
+        if (e != hipSuccess) return hip_fail(e, what);
+    }
+    return ok();
+}
+
+// ------------------------------------------------------------- dispatch
+
+int64_t iabs64(int64_t v) { return v < 0 ? -v : v; }
+
+// A kernel-frame operand: R rows, K contraction; element (r, p) at
+// p_ + r*rs + p*ks (elements); batch element z adds z*bs.
+struct Opnd {
+    const void *p;
+    int64_t rs, ks, bs;
+};
+
+bool canonical(const Opnd &o, int64_t R, int64_t K, size_t esz, int64_t batch) {
+    if (K * (int64_t)esz % 16 != 0) return false;
+    if (o.ks != 1 && K > 1) return false;
+    if ((uintptr_t)o.p % 16 != 0) return false;
+    if (R > 1 && (o.rs * (int64_t)esz) % 16 != 0) return false;
+    if (batch > 1 && (o.bs * (int64_t)esz) % 16 != 0) return false;
+    return true;
+}
+
+int64_t round_up64(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+// Brings an operand into the k-contiguous layout, packing into `dst` when its
+// own strides do not allow it.  Returns the (possibly new) operand.
+int materialize(InType in, const Opnd &o, int64_t R, int64_t K, int64_t batch, uint8_t *dst,
+                Opnd *out) {
+    const size_t esz = in_size(in);
+    const int64_t ld = round_up64(std::max<int64_t>(K, 1), 16 / (int64_t)esz);
+    const int64_t nb = (batch > 1 && o.bs != 0) ? batch : 1;
+    for (int64_t z = 0; z < nb; ++z) {
+        const uint8_t *src = (const uint8_t *)o.p + z * o.bs * (int64_t)esz;
+        hipError_t e = launch_pack(in, src, o.rs, o.ks, R, K, dst + z * R * ld * (int64_t)esz, ld,
+                                   tl_stream);
+        if (e != hipSuccess) return hip_fail(e, "pack");
+    }
+    *out = Opnd{dst, ld, 1, nb > 1 ? R * ld : 0};
+    return GK_OK;
+}
+
+size_t pack_bytes(InType in, int64_t R, int64_t K, int64_t batch, const Opnd &o) {
+    const size_t esz = in_size(in);
+    const int64_t ld = round_up64(std::max<int64_t>(K, 1), 16 / (int64_t)esz);
+    const int64_t nb = (batch > 1 && o.bs != 0) ? batch : 1;
+    return (size_t)round_up64(nb * R * ld * (int64_t)esz, 256);
+}
+
+Tile env_tile(bool *forced) {
+    const char *s = getenv("GEMMKIT_HIP_TILE");
+    *forced = false;
+    if (!s) return Tile::T256x256;
+    *forced = true;
+    if (!strcmp(s, "256x256")) return Tile::T256x256;
+    if (!strcmp(s, "256x128")) return Tile::T256x128;
+    if (!strcmp(s, "128x128")) return Tile::T128x128;
+    if (!strcmp(s, "64x64")) return Tile::T64x64;
+    *forced = false;
+    return Tile::T256x256;
+}
+
+// Tile table: per shape, the tile that minimises waves x per-wave work, where
+// a CU holds `occ` workgroups of a tile at once and `eff` is the tile's
+// relative matrix-core efficiency.
+Tile pick_tile(int64_t M, int64_t N, int64_t batch) {
+    bool forced;
+    Tile t = env_tile(&forced);
+    if (forced) return t;
+    struct Cand { Tile t; int bm, bn, occ; double eff; };
+    static const Cand cands[] = {
+        {Tile::T256x256, 256, 256, 1, 1.00},
+        {Tile::T256x128, 256, 128, 1, 0.90},
+        {Tile::T128x128, 128, 128, 2, 0.75},
+        {Tile::T64x64, 64, 64, 4, 0.40},
+    };
+    double best = 1e300;
+    Tile bt = Tile::T64x64;
+    for (const Cand &c : cands) {
+        int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * batch;
+        int64_t slots = (int64_t)g_num_cus * c.occ;
+        int64_t waves = (tiles + slots - 1) / slots;
+        double cost = (double)waves * c.occ * c.bm * c.bn / c.eff;
+        if (cost < best * 0.999) { best = cost; bt = c.t; }
+    }
+    return bt;
+}
+
+// The shared core: C = epi(A*B) for every batch element.  `ep` comes in the
+// user frame (rsc/csc of the user's C, axis 0 = per user row); m, k, n >= 1.
+int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t k, int64_t n,
+                const void *a, int64_t rsa, int64_t csa, int64_t bsa, const void *b,
+                int64_t rsb, int64_t csb, int64_t bsb, void *c, int64_t rsc, int64_t csc,
+                int64_t bsc, int64_t batch, const gk_packed_rhs *packed = nullptr) {
+    const size_t esz = in_size(in);
+    // Orientation: the kernels write C row-major-ish (kernel column index the
+    // fast one), so a column-major-ish C computes C^T = B^T A^T -- a swap of
+    // roles only, both operands being read k-contiguous.
+    const bool swap = iabs64(csc) > iabs64(rsc);
+    Opnd A{a, rsa, csa, bsa};
+    Opnd Bt{b, csb, rsb, bsb};  // B^T: n x k
+    if (packed) Bt = Opnd{packed->buf, packed->ld, 1, 0};
+    int64_t M = m, N = n;
+    ep.c = c;
+    ep.bsc = bsc;
+    if (swap) {
+        std::swap(A, Bt);
+        std::swap(M, N);
+        ep.rsc = csc;
+        ep.csc = rsc;
+        ep.axis ^= 1;
+    } else {
+        ep.rsc = rsc;
+        ep.csc = csc;
+    }
+
+    gk_workspace *ws = resolve_ws(ws_in);
+    const bool a_ok = canonical(A, M, k, esz, batch);
+    const bool b_ok = canonical(Bt, N, k, esz, batch);
+    if (!a_ok || !b_ok) {
+        size_t need = (a_ok ? 0 : pack_bytes(in, M, k, batch, A)) +
+                      (b_ok ? 0 : pack_bytes(in, N, k, batch, Bt));
+        void *base = nullptr;
+        int r = ws_reserve(ws, need, &base);
+        if (r) return r;
+        uint8_t *dst = (uint8_t *)base;
+        if (!a_ok) {
+            size_t used = pack_bytes(in, M, k, batch, A);
+            if ((r = materialize(in, A, M, k, batch, dst, &A))) return r;
+            dst += used;
+        }
+        if (!b_ok && (r = materialize(in, Bt, N, k, batch, dst, &Bt))) return r;
+    }
+
+    hipError_t e;
+    if ((M <= 8 || N <= 8) && std::max(M, N) >= 1) {
+        // GEMV route: the short side's rows are the vectors.
+        GemvArgs g{};
+        EpiParams eg = ep;
+        if (M <= 8) {
+            g.mat = Bt.p; g.ld = Bt.rs; g.vec = A.p; g.vld = A.rs; g.R = (int32_t)N; g.nvec = (int32_t)M;
+        } else {
+            g.mat = A.p; g.ld = A.rs; g.vec = Bt.p; g.vld = Bt.rs; g.R = (int32_t)M; g.nvec = (int32_t)N;
+            std::swap(eg.rsc, eg.csc);
+            eg.axis ^= 1;
+        }
+        g.K = (int32_t)k;
+        const Opnd &mat = (M <= 8) ? Bt : A;
+        const Opnd &vec = (M <= 8) ? A : Bt;
+        for (int64_t z = 0; z < batch; ++z) {
+            GemvArgs gz = g;
+            gz.mat = (const uint8_t *)mat.p + z * mat.bs * (int64_t)esz;
+            gz.vec = (const uint8_t *)vec.p + z * vec.bs * (int64_t)esz;
+            EpiParams ez = eg;
+            ez.c = (uint8_t *)ep.c + z * bsc * (int64_t)(ep.kind == EpiKind::Q8 ? 1 : (ep.kind == EpiKind::BF16 ? 2 : 4));
+            e = launch_gemv(in, gz, ez, tl_stream);
+            if (e != hipSuccess) return hip_fail(e, "gemv launch");
+        }
+        return finish("gemv");
+    }
+
+    MmaArgs args{};
+    args.a = A.p;
+    args.b = Bt.p;
+    args.lda = A.rs;
+    args.ldb = Bt.rs;
+    args.bsa = A.bs;
+    args.bsb = Bt.bs;
+    args.M = (int32_t)M;
+    args.N = (int32_t)N;
+    args.K = (int32_t)k;
+    args.batch = (int32_t)batch;
+    e = launch_mma(in, pick_tile(M, N, batch), args, ep, tl_stream);
+    if (e != hipSuccess) return hip_fail(e, "mfma launch");
+    return finish("mfma gemm");
+}
+
+bool dims_fit(size_t m, size_t k, size_t n, size_t batch) {
+    const size_t lim = (size_t)INT32_MAX;
+    return m <= lim && k <= lim && n <= lim && batch <= 65535;
+}
+
+// Degenerate C <- beta*C (k == 0 or alpha == 0).
+int scale_c(EpiKind kind, void *c, size_t m, size_t n, ptrdiff_t rsc, ptrdiff_t csc,
+            size_t batch, ptrdiff_t bsc, int32_t beta_i, float beta_f) {
+    bool one = (kind == EpiKind::I32) ? beta_i == 1 : beta_f == 1.0f;
+    if (one) return ok();
+    hipError_t e = launch_scale_c(kind, c, (int64_t)m, (int64_t)n, rsc, csc, (int64_t)batch, bsc,
+                                  beta_i, beta_f, tl_stream);
+    if (e != hipSuccess) return hip_fail(e, "scale_c launch");
+    return finish("scale_c");
+}
+
+EpiParams epi_int(int32_t alpha, int32_t beta) {
+    EpiParams ep{};
+    ep.kind = EpiKind::I32;
+    ep.alpha_i = alpha;
+    ep.beta_i = beta;
+    return ep;
+}
+
+EpiParams epi_float(EpiKind kind, float alpha, float beta) {
+    EpiParams ep{};
+    ep.kind = kind;
+    ep.alpha_f = alpha;
+    ep.beta_f = beta;
+    return ep;
+}
+
+float bf16_to_f32(gk_bf16 h) {
+    uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+// ---- i8 -> i32 core (execute_int, src/dispatch/int.rs:131-148)
+int exec_i8(gk_workspace *ws, size_t m, size_t k, size_t n, int32_t alpha, const int8_t *a,
+            ptrdiff_t rsa, ptrdiff_t csa, const int8_t *b, ptrdiff_t rsb, ptrdiff_t csb,
+            int32_t beta, int32_t *c, ptrdiff_t rsc, ptrdiff_t csc,
+            const gk_packed_rhs *packed = nullptr) {
+    int r;
+    if ((r = device_init())) return r;
+    if (m == 0 || n == 0) return ok();
+    if (!dims_fit(m, k, n, 1)) return fail(GK_ERR_OVERFLOW, "gemmkit: dimensions exceed 2^31-1");
+    if (k == 0 || alpha == 0) return scale_c(EpiKind::I32, c, m, n, rsc, csc, 1, 0, beta, 0.f);
+    return run_product(ws, InType::I8, epi_int(alpha, beta), m, k, n, a, rsa, csa, 0, b, rsb, csb,
+                       0, c, rsc, csc, 0, 1, packed);
+}
+
+// ---- float-family core (execute, src/dispatch.rs:345-358)
+int exec_float(gk_workspace *ws, InType in, EpiKind kind, size_t batch, size_t m, size_t k,
+               size_t n, float alpha, const void *a, ptrdiff_t rsa, ptrdiff_t csa, ptrdiff_t bsa,
+               const void *b, ptrdiff_t rsb, ptrdiff_t csb, ptrdiff_t bsb, float beta, void *c,
+               ptrdiff_t rsc, ptrdiff_t csc, ptrdiff_t bsc) {
+    int r;
+    if ((r = device_init())) return r;
+    if (batch == 0 || m == 0 || n == 0) return ok();
+    if (!dims_fit(m, k, n, batch)) return fail(GK_ERR_OVERFLOW, "gemmkit: dimensions exceed 2^31-1");
+    if (k == 0 || alpha == 0.0f) return scale_c(kind, c, m, n, rsc, csc, batch, bsc, 0, beta);
+    return run_product(ws, in, epi_float(kind, alpha, beta), m, k, n, a, rsa, csa, bsa, b, rsb,
+                       csb, bsb, c, rsc, csc, bsc, batch);
+}
+
+// ---- requant core (execute_int_requant, src/dispatch/int.rs:672-700)
+int exec_requant(gk_workspace *ws, size_t m, size_t k, size_t n, const int8_t *a, ptrdiff_t rsa,
+                 ptrdiff_t csa, const int8_t *b, ptrdiff_t rsb, ptrdiff_t csb, float scale,
+                 const float *scales, int32_t zp, const int32_t *bias, int32_t axis, int32_t act,
+                 int32_t lo, int32_t hi, void *c, ptrdiff_t rsc, ptrdiff_t csc,
+                 const gk_packed_rhs *packed = nullptr) {
+    int r;
+    if ((r = device_init())) return r;
+    if (axis != GK_AXIS_ROW && axis != GK_AXIS_COL)
+        return fail(GK_ERR_ARG, "gemmkit: requantize axis (%d) must be 0 (per-row) or 1 (per-col)", axis);
+    if (act != GK_ACT_NONE && act != GK_ACT_RELU)
+        return fail(GK_ERR_ARG, "gemmkit: requantize act (%d) must be 0 (none) or 1 (relu)", act);
+    if (m == 0 || n == 0) return ok();
+    if (!dims_fit(m, k, n, 1)) return fail(GK_ERR_OVERFLOW, "gemmkit: dimensions exceed 2^31-1");
+    EpiParams ep{};
+    ep.kind = EpiKind::Q8;
+    ep.scale = scale;
+    ep.scales = scales;
+    ep.bias = bias;
+    ep.axis = axis;
+    ep.zp = zp;
+    ep.lo = (act == GK_ACT_RELU) ? std::max(lo, zp) : lo;
+    ep.hi = hi;
+    if (k == 0) {
+        ep.c = c;
+        ep.rsc = rsc;
+        ep.csc = csc;
+        hipError_t e = launch_requant_fill(ep, (int64_t)m, (int64_t)n, tl_stream);
+        if (e != hipSuccess) return hip_fail(e, "requant fill launch");
+        return finish("requant fill");
+    }
+    return run_product(ws, InType::I8, ep, m, k, n, a, rsa, csa, 0, b, rsb, csb, 0, c, rsc, csc,
+                       0, 1, packed);
+}
+
+// requant_scale / requant_bias / zero-point checks (src/adapter.rs:190-273,
+// src/api/int8.rs:291-295, :506-510).  `chan` is the channel count of the
+// chosen axis; `axis_name` is "A.rows" for the reference's per-row vectors.
+int validate_requant(const gk_requantize *req, const gk_mat_mut *c, size_t m, size_t n, bool u8) {
+    if (!req) return fail(GK_ERR_ARG, "gemmkit: null requantize argument");
+    if (req->axis != GK_AXIS_ROW && req->axis != GK_AXIS_COL)
+        return fail(GK_ERR_ARG, "gemmkit: requantize axis (%d) must be 0 (per-row) or 1 (per-col)",
+                    req->axis);
+    if (req->act != GK_ACT_NONE && req->act != GK_ACT_RELU)
+        return fail(GK_ERR_ARG, "gemmkit: requantize act (%d) must be 0 (none) or 1 (relu)", req->act);
+    const size_t chan = req->axis == GK_AXIS_ROW ? m : n;
+    const char *axis_name = req->axis == GK_AXIS_ROW ? "A.rows" : "B.cols";
+    if (!req->scales) {
+        float s = req->scale;
+        if (!(std::isfinite(s) && s > 0.0f))
+            return fail(GK_ERR_ARG, "gemmkit: requantize scale (%s) must be finite and > 0",
+                        rust_f32(s).c_str());
+    } else {
+        if (req->scales_len != chan)
+            return fail(GK_ERR_SHAPE, "gemmkit: requantize scales length (%zu) != %s (%zu)",
+                        req->scales_len, axis_name, chan);
+        if (overlaps_bytes(c->data, c->len, 1, req->scales, req->scales_len, 4))
+            return fail(GK_ERR_ALIAS, "gemmkit: requantize scales overlap C");
+        // The scale values live in device memory: copy them back to check.
+        if (chan > 0) {
+            float *h = (float *)malloc(chan * sizeof(float));
+            if (!h) return fail(GK_ERR_NOMEM, "gemmkit: host allocation failed");
+            hipError_t e = hipMemcpy(h, req->scales, chan * sizeof(float), hipMemcpyDeviceToHost);
+            if (e != hipSuccess) {
+                free(h);
+                return hip_fail(e, "requantize scale check");
+            }
+            for (size_t i = 0; i < chan; ++i) {
+                if (!(std::isfinite(h[i]) && h[i] > 0.0f)) {
+                    std::string t = rust_f32(h[i]);
+                    free(h);
+                    return fail(GK_ERR_ARG, "gemmkit: requantize scale (%s) must be finite and > 0",
+                                t.c_str());
+                }
+            }
+            free(h);
+        }
+    }
+    if (u8) {
+        if (req->zero_point < 0 || req->zero_point > 255)
+            return fail(GK_ERR_ARG, "gemmkit: requantize zero_point (%d) out of u8 range [0, 255]",
+                        req->zero_point);
+    } else if (req->zero_point < -128 || req->zero_point > 127) {
+        return fail(GK_ERR_ARG, "gemmkit: requantize zero_point (%d) out of i8 range [-128, 127]",
+                    req->zero_point);
+    }
+    if (req->bias) {
+        if (req->bias_len != chan)
+            return fail(GK_ERR_SHAPE, "gemmkit: requantize bias length (%zu) != %s (%zu)",
+                        req->bias_len, axis_name, chan);
+        if (overlaps_bytes(c->data, c->len, 1, req->bias, req->bias_len, 4))
+            return fail(GK_ERR_ALIAS, "gemmkit: requantize bias overlaps C");
+    }
+    return GK_OK;
+}
+
+int requant_checked(gk_workspace *ws, const gk_mat_ref *a, const gk_mat_ref *b,
+                    const gk_packed_rhs *packed, const gk_requantize *req, const gk_mat_mut *c,
+                    bool u8) {
+    int r;
+    if (packed) {
+        if (!a || !c) return fail(GK_ERR_ARG, "gemmkit: null view argument");
+        if (a->cols != packed->k)
+            return fail(GK_ERR_SHAPE, "gemmkit: A.cols (%zu) != packed B.rows (%zu)", a->cols, packed->k);
+        if (packed->n != c->cols)
+            return fail(GK_ERR_SHAPE, "gemmkit: packed B.cols (%zu) != C.cols (%zu)", packed->n, c->cols);
+        if (a->rows != c->rows)
+            return fail(GK_ERR_SHAPE, "gemmkit: A.rows (%zu) != C.rows (%zu)", a->rows, c->rows);
+        if ((r = check_view(a->len, a->rows, a->cols, a->rs, a->cs, "A"))) return r;
+        if ((r = check_view(c->len, c->rows, c->cols, c->rs, c->cs, "C"))) return r;
+        if (self_aliases(c->rows, c->cols, c->rs, c->cs))
+            return fail(GK_ERR_ALIAS,
+                        "gemmkit: C view aliases itself (strides %td,%td map distinct elements to "
+                        "the same memory); C must address each (i,j) uniquely",
+                        c->rs, c->cs);
+        if (overlaps_bytes(c->data, c->len, 1, a->data, a->len, 1))
+            return fail(GK_ERR_ALIAS, "gemmkit: C aliases A");
+    } else if ((r = validate_gemm_views(a, b, c, 1, 1))) {
+        return r;
+    }
+    const size_t m = a->rows, k = a->cols, n = c->cols;
+    if ((r = validate_requant(req, c, m, n, u8))) return r;
+    const int8_t *bp = packed ? nullptr : (const int8_t *)b->data;
+    return exec_requant(ws, m, k, n, (const int8_t *)a->data, a->rs, a->cs, bp,
+                        packed ? 0 : b->rs, packed ? 0 : b->cs, req->scale, req->scales,
+                        req->zero_point, req->bias, req->axis, req->act, u8 ? 0 : -128,
+                        u8 ? 255 : 127, c->data, c->rs, c->cs, packed);
+}
+
+// check_batched_view (src/api/batched.rs:31-69); returns the element extent.
+int check_batched_view(size_t len, size_t rows, size_t cols, ptrdiff_t rs, ptrdiff_t cs,
+                       size_t batch, ptrdiff_t bs, const char *name, size_t *ext) {
+    size_t e = 0;
+    if (!extent(rows, cols, rs, cs, &e))
+        return fail(GK_ERR_VIEW,
+                    "gemmkit: %s view has negative strides or is too large to address; use the "
+                    "unchecked API",
+                    name);
+    size_t last_base = 0;
+    if (batch > 1) {
+        if (bs < 0)
+            return fail(GK_ERR_VIEW, "gemmkit: %s batch stride (%td) must be non-negative", name, bs);
+        __int128 lb = (__int128)(batch - 1) * (size_t)bs;
+        last_base = lb > (__int128)SIZE_MAX ? SIZE_MAX : (size_t)lb;
+    }
+    size_t need = last_base > SIZE_MAX - e ? SIZE_MAX : last_base + e;
+    if (need > len)
+        return fail(GK_ERR_VIEW,
+                    "gemmkit: %s batched view (%zu\xC3\x97 %zux%zu, batch stride %td) needs %zu "
+                    "elements but slice has %zu",
+                    name, batch, rows, cols, bs, need, len);
+    *ext = e;
+    return GK_OK;
+}
+
+// validate_batched_views (src/api/batched.rs:78-163).
+int validate_batched_views(size_t batch, const gk_mat_ref *a, ptrdiff_t a_bs, const gk_mat_ref *b,
+                           ptrdiff_t b_bs, const gk_mat_mut *c, ptrdiff_t c_bs, size_t si,
+                           size_t so) {
+    if (!a || !b || !c) return fail(GK_ERR_ARG, "gemmkit: null view argument");
+    if (a->cols != b->rows)
+        return fail(GK_ERR_SHAPE, "gemmkit: A.cols (%zu) != B.rows (%zu)", a->cols, b->rows);
+    if (a->rows != c->rows)
+        return fail(GK_ERR_SHAPE, "gemmkit: A.rows (%zu) != C.rows (%zu)", a->rows, c->rows);
+    if (b->cols != c->cols)
+        return fail(GK_ERR_SHAPE, "gemmkit: B.cols (%zu) != C.cols (%zu)", b->cols, c->cols);
+    size_t ea, eb, ec;
+    int r;
+    if ((r = check_batched_view(a->len, a->rows, a->cols, a->rs, a->cs, batch, a_bs, "A", &ea))) return r;
+    if ((r = check_batched_view(b->len, b->rows, b->cols, b->rs, b->cs, batch, b_bs, "B", &eb))) return r;
+    if ((r = check_batched_view(c->len, c->rows, c->cols, c->rs, c->cs, batch, c_bs, "C", &ec))) return r;
+    if (self_aliases(c->rows, c->cols, c->rs, c->cs))
+        return fail(GK_ERR_ALIAS,
+                    "gemmkit: batched C element aliases itself (strides %td,%td map distinct "
+                    "elements to the same memory); C must address each (i,j) uniquely",
+                    c->rs, c->cs);
+    if (batch > 1 && (size_t)c_bs < ec)
+        return fail(GK_ERR_ALIAS,
+                    "gemmkit: C batch stride (%td) must be at least the element extent (%zu) so "
+                    "the batched C outputs stay disjoint",
+                    c_bs, ec);
+    if (overlaps_bytes(c->data, c->len, so, a->data, a->len, si) ||
+        overlaps_bytes(c->data, c->len, so, b->data, b->len, si))
+        return fail(GK_ERR_ALIAS, "gemmkit: batched C aliases A or B");
+    return GK_OK;
+}
+
+}  // namespace
+
+// =============================================================== C ABI
+
+extern "C" {
+
+const char *gk_last_error(void) { return tl_error.c_str(); }
+
+const char *gk_version(void) { return "gemmkit-hip 0.1.0 (gfx950)"; }
+
+int gk_init(void) {
+    int r = device_init();
+    return r ? r : ok();
+}
+
+int gk_set_stream(void *hip_stream) {
+    tl_stream = (hipStream_t)hip_stream;
+    return ok();
+}
+
+void *gk_get_stream(void) { return (void *)tl_stream; }
+
+int gk_set_synchronous(int on) {
+    tl_sync = on ? 1 : 0;
+    return ok();
+}
+
+gk_workspace *gk_workspace_new(void) { return new gk_workspace(); }
+
+void gk_workspace_free(gk_workspace *ws) {
+    if (!ws) return;
+    if (ws->ptr) {
+        (void)hipDeviceSynchronize();
+        (void)hipFree(ws->ptr);
+    }
+    delete ws;
+}
+
+size_t gk_workspace_bytes(const gk_workspace *ws) { return ws ? ws->bytes : 0; }
+
+// ---- f32
+
+int gk_gemm_f32_unchecked(gk_workspace *ws, size_t m, size_t k, size_t n, float alpha,
+                          const float *a, ptrdiff_t rsa, ptrdiff_t csa, const float *b,
+                          ptrdiff_t rsb, ptrdiff_t csb, float beta, float *c, ptrdiff_t rsc,
+                          ptrdiff_t csc, gk_par) {
+    return exec_float(ws, InType::F32, EpiKind::F32, 1, m, k, n, alpha, a, rsa, csa, 0, b, rsb,
+                      csb, 0, beta, c, rsc, csc, 0);
+}
+
+int gk_gemm_f32(gk_workspace *ws, float alpha, const gk_mat_ref *a, const gk_mat_ref *b,
+                float beta, const gk_mat_mut *c, gk_par par) {
+    int r = validate_gemm_views(a, b, c, 4, 4);
+    if (r) return r;
+    return gk_gemm_f32_unchecked(ws, a->rows, a->cols, b->cols, alpha, (const float *)a->data,
+                                 a->rs, a->cs, (const float *)b->data, b->rs, b->cs, beta,
+                                 (float *)c->data, c->rs, c->cs, par);
+}
+
+// ---- bf16
+
+int gk_gemm_bf16_unchecked(gk_workspace *ws, size_t m, size_t k, size_t n, gk_bf16 alpha,
+                           const gk_bf16 *a, ptrdiff_t rsa, ptrdiff_t csa, const gk_bf16 *b,
+                           ptrdiff_t rsb, ptrdiff_t csb, gk_bf16 beta, gk_bf16 *c, ptrdiff_t rsc,
+                           ptrdiff_t csc, gk_par) {
+    return exec_float(ws, InType::BF16, EpiKind::BF16, 1, m, k, n, bf16_to_f32(alpha), a, rsa,
+                      csa, 0, b, rsb, csb, 0, bf16_to_f32(beta), c, rsc, csc, 0);
+}
+
+int gk_gemm_bf16(gk_workspace *ws, gk_bf16 alpha, const gk_mat_ref *a, const gk_mat_ref *b,
+                 gk_bf16 beta, const gk_mat_mut *c, gk_par par) {
+    int r = validate_gemm_views(a, b, c, 2, 2);
+    if (r) return r;
+    return gk_gemm_bf16_unchecked(ws, a->rows, a->cols, b->cols, alpha, (const gk_bf16 *)a->data,
+                                  a->rs, a->cs, (const gk_bf16 *)b->data, b->rs, b->cs, beta,
+                                  (gk_bf16 *)c->data, c->rs, c->cs, par);
+}
+
+int gk_gemm_bf16_f32out_unchecked(gk_workspace *ws, size_t m, size_t k, size_t n, float alpha,
+                                  const gk_bf16 *a, ptrdiff_t rsa, ptrdiff_t csa,
+                                  const gk_bf16 *b, ptrdiff_t rsb, ptrdiff_t csb, float beta,
+                                  float *c, ptrdiff_t rsc, ptrdiff_t csc, gk_par) {
+    return exec_float(ws, InType::BF16, EpiKind::F32, 1, m, k, n, alpha, a, rsa, csa, 0, b, rsb,
+                      csb, 0, beta, c, rsc, csc, 0);
+}
+
+int gk_gemm_bf16_f32out(gk_workspace *ws, float alpha, const gk_mat_ref *a, const gk_mat_ref *b,
+                        float beta, const gk_mat_mut *c, gk_par par) {
+    int r = validate_gemm_views(a, b, c, 2, 4);
+    if (r) return r;
+    return gk_gemm_bf16_f32out_unchecked(ws, a->rows, a->cols, b->cols, alpha,
+                                         (const gk_bf16 *)a->data, a->rs, a->cs,
+                                         (const gk_bf16 *)b->data, b->rs, b->cs, beta,
+                                         (float *)c->data, c->rs, c->cs, par);
+}
+
+// ---- i8
+
+int gk_gemm_i8_unchecked(gk_workspace *ws, size_t m, size_t k, size_t n, int32_t alpha,
+                         const int8_t *a, ptrdiff_t rsa, ptrdiff_t csa, const int8_t *b,
+                         ptrdiff_t rsb, ptrdiff_t csb, int32_t beta, int32_t *c, ptrdiff_t rsc,
+                         ptrdiff_t csc, gk_par) {
+    return exec_i8(ws, m, k, n, alpha, a, rsa, csa, b, rsb, csb, beta, c, rsc, csc);
+}
+
+int gk_gemm_i8(gk_workspace *ws, int32_t alpha, const gk_mat_ref *a, const gk_mat_ref *b,
+               int32_t beta, const gk_mat_mut *c, gk_par par) {
+    int r = validate_gemm_views(a, b, c, 1, 4);
+    if (r) return r;
+    return gk_gemm_i8_unchecked(ws, a->rows, a->cols, b->cols, alpha, (const int8_t *)a->data,
+                                a->rs, a->cs, (const int8_t *)b->data, b->rs, b->cs, beta,
+                                (int32_t *)c->data, c->rs, c->cs, par);
+}
+
+// ---- requant
+
+int gk_gemm_i8_requant(gk_workspace *ws, const gk_mat_ref *a, const gk_mat_ref *b,
+                       const gk_requantize *req, const gk_mat_mut *c, gk_par) {
+    return requant_checked(ws, a, b, nullptr, req, c, false);
+}
+
+int gk_gemm_i8_requant_u8(gk_workspace *ws, const gk_mat_ref *a, const gk_mat_ref *b,
+                          const gk_requantize *req, const gk_mat_mut *c, gk_par) {
+    return requant_checked(ws, a, b, nullptr, req, c, true);
+}
+
+int gk_gemm_i8_requant_unchecked(gk_workspace *ws, size_t m, size_t k, size_t n, const int8_t *a,
+                                 ptrdiff_t rsa, ptrdiff_t csa, const int8_t *b, ptrdiff_t rsb,
+                                 ptrdiff_t csb, float scale, const float *row_scales,
+                                 uint8_t has_row_scales, int32_t zero_point, const int32_t *bias,
+                                 uint8_t has_bias, int8_t *c, ptrdiff_t rsc, ptrdiff_t csc, gk_par,
+                                 int32_t axis, int32_t act) {
+    return exec_requant(ws, m, k, n, a, rsa, csa, b, rsb, csb, scale,
+                        has_row_scales ? row_scales : nullptr, zero_point,
+                        has_bias ? bias : nullptr, axis, act, -128, 127, c, rsc, csc);
+}
+
+int gk_gemm_i8_requant_u8_unchecked(gk_workspace *ws, size_t m, size_t k, size_t n,
+                                    const int8_t *a, ptrdiff_t rsa, ptrdiff_t csa,
+                                    const int8_t *b, ptrdiff_t rsb, ptrdiff_t csb, float scale,
+                                    const float *row_scales, uint8_t has_row_scales,
+                                    int32_t zero_point, const int32_t *bias, uint8_t has_bias,
+                                    uint8_t *c, ptrdiff_t rsc, ptrdiff_t csc, gk_par, int32_t axis,
+                                    int32_t act) {
+    return exec_requant(ws, m, k, n, a, rsa, csa, b, rsb, csb, scale,
+                        has_row_scales ? row_scales : nullptr, zero_point,
+                        has_bias ? bias : nullptr, axis, act, 0, 255, c, rsc, csc);
+}
+
+// ---- prepacked RHS (src/api/packed.rs:372-656)
+
+int gk_prepack_rhs_i8_unchecked(const int8_t *b, ptrdiff_t rsb, ptrdiff_t csb, size_t k, size_t n,
+                                gk_packed_rhs **out) {
+    int r;
+    if (!out) return fail(GK_ERR_ARG, "gemmkit: null output handle");
+    *out = nullptr;
+    if ((r = device_init())) return r;
+    if (!dims_fit(1, k, n, 1)) return fail(GK_ERR_OVERFLOW, "gemmkit: prepacked RHS of %zux%zu is too large; the pack buffer size overflows usize", k, n);
+    gk_packed_rhs *p = new gk_packed_rhs();
+    p->k = k;
+    p->n = n;
+    p->ld = round_up64(std::max<int64_t>((int64_t)k, 1), 16);
+    if (k > 0 && n > 0) {
+        size_t bytes = (size_t)p->ld * n;
+        hipError_t e = hipMalloc((void **)&p->buf, bytes);
+        if (e != hipSuccess) {
+            delete p;
+            return fail(GK_ERR_NOMEM, "gemmkit: prepacked RHS allocation of %zu bytes failed", bytes);
+        }
+        // Store B^T (n x k) k-contiguous: row j of the buffer is column j of B.
+        e = launch_pack(InType::I8, b, csb, rsb, (int64_t)n, (int64_t)k, p->buf, p->ld, tl_stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(tl_stream);
+        if (e != hipSuccess) {
+            (void)hipFree(p->buf);
+            delete p;
+            return hip_fail(e, "prepack");
+        }
+    }
+    *out = p;
+    return ok();
+}
+
+int gk_prepack_rhs_i8(const gk_mat_ref *b, gk_packed_rhs **out) {
+    if (!b) return fail(GK_ERR_ARG, "gemmkit: null view argument");
+    int r = check_view(b->len, b->rows, b->cols, b->rs, b->cs, "B");
+    if (r) return r;
+    return gk_prepack_rhs_i8_unchecked((const int8_t *)b->data, b->rs, b->cs, b->rows, b->cols, out);
+}
+
+void gk_packed_rhs_free(gk_packed_rhs *p) {
+    if (!p) return;
+    if (p->buf) {
+        (void)hipDeviceSynchronize();
+        (void)hipFree(p->buf);
+    }
+    delete p;
+}
+
+size_t gk_packed_rhs_rows(const gk_packed_rhs *p) { return p ? p->k : 0; }
+size_t gk_packed_rhs_cols(const gk_packed_rhs *p) { return p ? p->n : 0; }
+
+int gk_gemm_i8_packed_b_unchecked(gk_workspace *ws, int32_t alpha, size_t m, const int8_t *a,
+                                  ptrdiff_t rsa, ptrdiff_t csa, const gk_packed_rhs *packed,
+                                  int32_t beta, int32_t *c, ptrdiff_t rsc, ptrdiff_t csc, gk_par) {
+    if (!packed) return fail(GK_ERR_ARG, "gemmkit: null packed RHS");
+    // Same orientation rule as the reference (src/api/packed.rs:625-629).
+    if ((csc < 0 ? -csc : csc) < (rsc < 0 ? -rsc : rsc))
+        return fail(GK_ERR_LAYOUT,
+                    "gemmkit: gemm_packed_b requires column-major-ish C (|csc| >= |rsc|); a "
+                    "row-major C would swap A/B and invalidate the prepacked RHS \xE2\x80\x94 use "
+                    "gemm() for that layout");
+    return exec_i8(ws, m, packed->k, packed->n, alpha, a, rsa, csa, nullptr, 0, 0, beta, c, rsc,
+                   csc, packed);
+}
+
+int gk_gemm_i8_packed_b(gk_workspace *ws, int32_t alpha, const gk_mat_ref *a,
+                        const gk_packed_rhs *packed, int32_t beta, const gk_mat_mut *c,
+                        gk_par par) {
+    if (!a || !c || !packed) return fail(GK_ERR_ARG, "gemmkit: null argument");
+    if (a->cols != packed->k)
+        return fail(GK_ERR_SHAPE, "gemmkit: A.cols (%zu) != packed B.rows (%zu)", a->cols, packed->k);
+    if (packed->n != c->cols)
+        return fail(GK_ERR_SHAPE, "gemmkit: packed B.cols (%zu) != C.cols (%zu)", packed->n, c->cols);
+    if (a->rows != c->rows)
+        return fail(GK_ERR_SHAPE, "gemmkit: A.rows (%zu) != C.rows (%zu)", a->rows, c->rows);
+    int r;
+    if ((r = check_view(a->len, a->rows, a->cols, a->rs, a->cs, "A"))) return r;
+    if ((r = check_view(c->len, c->rows, c->cols, c->rs, c->cs, "C"))) return r;
+    if (self_aliases(c->rows, c->cols, c->rs, c->cs))
+        return fail(GK_ERR_ALIAS,
+                    "gemmkit: C view aliases itself (strides %td,%td map distinct elements to the "
+                    "same memory); C must address each (i,j) uniquely",
+                    c->rs, c->cs);
+    if (overlaps_bytes(c->data, c->len, 4, a->data, a->len, 1))
+        return fail(GK_ERR_ALIAS, "gemmkit: C aliases A");
+    return gk_gemm_i8_packed_b_unchecked(ws, alpha, a->rows, (const int8_t *)a->data, a->rs, a->cs,
+                                         packed, beta, (int32_t *)c->data, c->rs, c->cs, par);
+}
+
+int gk_gemm_i8_packed_b_requant(gk_workspace *ws, const gk_mat_ref *a, const gk_packed_rhs *packed,
+                                const gk_requantize *req, const gk_mat_mut *c, gk_par) {
+    if (!packed) return fail(GK_ERR_ARG, "gemmkit: null packed RHS");
+    return requant_checked(ws, a, nullptr, packed, req, c, false);
+}
+
+int gk_gemm_i8_packed_b_requant_u8(gk_workspace *ws, const gk_mat_ref *a,
+                                   const gk_packed_rhs *packed, const gk_requantize *req,
+                                   const gk_mat_mut *c, gk_par) {
+    if (!packed) return fail(GK_ERR_ARG, "gemmkit: null packed RHS");
+    return requant_checked(ws, a, nullptr, packed, req, c, true);
+}
+
+// ---- batched (src/api/batched.rs:188-711)
+
+int gk_gemm_batched_f32_unchecked(gk_workspace *ws, size_t batch, size_t m, size_t k, size_t n,
+                                  float alpha, const float *a, ptrdiff_t rsa, ptrdiff_t csa,
+                                  ptrdiff_t a_bs, const float *b, ptrdiff_t rsb, ptrdiff_t csb,
+                                  ptrdiff_t b_bs, float beta, float *c, ptrdiff_t rsc,
+                                  ptrdiff_t csc, ptrdiff_t c_bs, gk_par) {
+    return exec_float(ws, InType::F32, EpiKind::F32, batch, m, k, n, alpha, a, rsa, csa, a_bs, b,
+                      rsb, csb, b_bs, beta, c, rsc, csc, c_bs);
+}
+
+int gk_gemm_batched_f32(gk_workspace *ws, size_t batch, float alpha, const gk_mat_ref *a,
+                        ptrdiff_t a_bs, const gk_mat_ref *b, ptrdiff_t b_bs, float beta,
+                        const gk_mat_mut *c, ptrdiff_t c_bs, gk_par par) {
+    if (batch == 0) return ok();
+    int r = validate_batched_views(batch, a, a_bs, b, b_bs, c, c_bs, 4, 4);
+    if (r) return r;
+    return gk_gemm_batched_f32_unchecked(ws, batch, a->rows, a->cols, b->cols, alpha,
+                                         (const float *)a->data, a->rs, a->cs, a_bs,
+                                         (const float *)b->data, b->rs, b->cs, b_bs, beta,
+                                         (float *)c->data, c->rs, c->cs, c_bs, par);
+}
+
+int gk_gemm_batched_bf16_unchecked(gk_workspace *ws, size_t batch, size_t m, size_t k, size_t n,
+                                   gk_bf16 alpha, const gk_bf16 *a, ptrdiff_t rsa, ptrdiff_t csa,
+                                   ptrdiff_t a_bs, const gk_bf16 *b, ptrdiff_t rsb, ptrdiff_t csb,
+                                   ptrdiff_t b_bs, gk_bf16 beta, gk_bf16 *c, ptrdiff_t rsc,
+                                   ptrdiff_t csc, ptrdiff_t c_bs, gk_par) {
+    return exec_float(ws, InType::BF16, EpiKind::BF16, batch, m, k, n, bf16_to_f32(alpha), a, rsa,
+                      csa, a_bs, b, rsb, csb, b_bs, bf16_to_f32(beta), c, rsc, csc, c_bs);
+}
+
+int gk_gemm_batched_bf16(gk_workspace *ws, size_t batch, gk_bf16 alpha, const gk_mat_ref *a,
+                         ptrdiff_t a_bs, const gk_mat_ref *b, ptrdiff_t b_bs, gk_bf16 beta,
+                         const gk_mat_mut *c, ptrdiff_t c_bs, gk_par par) {
+    if (batch == 0) return ok();
+    int r = validate_batched_views(batch, a, a_bs, b, b_bs, c, c_bs, 2, 2);
+    if (r) return r;
+    return gk_gemm_batched_bf16_unchecked(ws, batch, a->rows, a->cols, b->cols, alpha,
+                                          (const gk_bf16 *)a->data, a->rs, a->cs, a_bs,
+                                          (const gk_bf16 *)b->data, b->rs, b->cs, b_bs, beta,
+                                          (gk_bf16 *)c->data, c->rs, c->cs, c_bs, par);
+}
+
+int gk_gemm_batched_bf16_f32out_unchecked(gk_workspace *ws, size_t batch, size_t m, size_t k,
+                                          size_t n, float alpha, const gk_bf16 *a, ptrdiff_t rsa,
+                                          ptrdiff_t csa, ptrdiff_t a_bs, const gk_bf16 *b,
+                                          ptrdiff_t rsb, ptrdiff_t csb, ptrdiff_t b_bs, float beta,
+                                          float *c, ptrdiff_t rsc, ptrdiff_t csc, ptrdiff_t c_bs,
+                                          gk_par) {
+    return exec_float(ws, InType::BF16, EpiKind::F32, batch, m, k, n, alpha, a, rsa, csa, a_bs, b,
+                      rsb, csb, b_bs, beta, c, rsc, csc, c_bs);
+}
+
+int gk_gemm_batched_bf16_f32out(gk_workspace *ws, size_t batch, float alpha, const gk_mat_ref *a,
+                                ptrdiff_t a_bs, const gk_mat_ref *b, ptrdiff_t b_bs, float beta,
+                                const gk_mat_mut *c, ptrdiff_t c_bs, gk_par par) {
+    if (batch == 0) return ok();
+    int r = validate_batched_views(batch, a, a_bs, b, b_bs, c, c_bs, 2, 4);
+    if (r) return r;
+    return gk_gemm_batched_bf16_f32out_unchecked(ws, batch, a->rows, a->cols, b->cols, alpha,
+                                                 (const gk_bf16 *)a->data, a->rs, a->cs, a_bs,
+                                                 (const gk_bf16 *)b->data, b->rs, b->cs, b_bs,
+                                                 beta, (float *)c->data, c->rs, c->cs, c_bs, par);
+}
+
+}  // extern "C"

@@ -1,0 +1,114 @@
+// epilogue.h -- per-element output maps applied to accumulator registers.
+//
+// Each map restates one of gemmkit's epilogues on a single accumulator value,
+// so the MFMA and GEMV kernels store through the same code:
+//   I32  int32_epilogue  (src/kernel/int.rs:36-120): alpha*acc, then C / C+acc /
+//        beta*C+acc, all wrapping i32;
+//   F32  the float epilogue (src/kernel/float.rs:150-281): alpha*acc, then
+//        beta*C + acc in f32 (beta == 0 never reads C);
+//   BF16 mixed_epilogue (src/kernel/mixed.rs:96-200): the f32 value of F32, then
+//        one round-to-nearest-even narrowing to bf16 with the NaN rule of
+//        src/simd/avx512.rs:194-212;
+//   Q8   KRequantize::apply (src/kernel/epilogue.rs:810-830): wrapping bias add,
+//        one f64 multiply by the widened f32 scale, round half to even, zero
+//        point, clamp to [lo, hi], store the low byte.
+#pragma once
+
+#include "internal.h"
+
+namespace gk {
+
+__device__ __forceinline__ uint16_t bf16_rne(float f) {
+    uint32_t bits = __float_as_uint(f);
+    if ((bits & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((bits >> 16) | 0x0040u);
+    uint32_t lsb = (bits >> 16) & 1u;
+    return (uint16_t)((bits + 0x7FFFu + lsb) >> 16);
+}
+
+__device__ __forceinline__ float bf16_widen(uint16_t h) {
+    return __uint_as_float((uint32_t)h << 16);
+}
+
+// The requant map on one i32 accumulator.  The product of an i32 and an f32,
+// both exact in f64, is one IEEE multiply; rint() is round-half-to-even under
+// the default rounding mode, and is the identity for |x| >= 2^52 exactly like
+// round_ne_f64's pass-through (src/kernel/epilogue.rs:886-897).  Adding zp in
+// f64 and clamping there equals the reference's saturating i64 add and clamp:
+// below 2^52 the sum is exact, above it both clamp to the band edge.
+__device__ __forceinline__ int32_t requant_value(int32_t acc, int32_t bias, float scale,
+                                                 int32_t zp, int32_t lo, int32_t hi) {
+#pragma clang fp contract(off)
+    int32_t v = (int32_t)((uint32_t)acc + (uint32_t)bias);
+    double x = (double)v * (double)scale;
+    double r = __builtin_rint(x);
+    r = r + (double)zp;
+    r = __builtin_fmax(r, (double)lo);
+    r = __builtin_fmin(r, (double)hi);
+    return (int32_t)r;
+}
+
+// Stores one accumulator at output coordinate (row, col) of batch element z.
+template <EpiKind K>
+struct Store;
+
+template <>
+struct Store<EpiKind::I32> {
+    __device__ __forceinline__ static void apply(const EpiParams &ep, int64_t z, int row, int col,
+                                                 int32_t acc) {
+        int32_t *c = (int32_t *)ep.c + z * ep.bsc + (int64_t)row * ep.rsc + (int64_t)col * ep.csc;
+        uint32_t v = (uint32_t)ep.alpha_i * (uint32_t)acc;
+        if (ep.beta_i == 0) {
+            *c = (int32_t)v;
+        } else if (ep.beta_i == 1) {
+            *c = (int32_t)((uint32_t)*c + v);
+        } else {
+            *c = (int32_t)((uint32_t)ep.beta_i * (uint32_t)*c + v);
+        }
+    }
+};
+
+template <>
+struct Store<EpiKind::F32> {
+    __device__ __forceinline__ static void apply(const EpiParams &ep, int64_t z, int row, int col,
+                                                 float acc) {
+        float *c = (float *)ep.c + z * ep.bsc + (int64_t)row * ep.rsc + (int64_t)col * ep.csc;
+        float v = ep.alpha_f * acc;
+        if (ep.beta_f == 0.0f) {
+            *c = v;
+        } else if (ep.beta_f == 1.0f) {
+            *c = *c + v;
+        } else {
+            *c = __builtin_fmaf(ep.beta_f, *c, v);
+        }
+    }
+};
+
+template <>
+struct Store<EpiKind::BF16> {
+    __device__ __forceinline__ static void apply(const EpiParams &ep, int64_t z, int row, int col,
+                                                 float acc) {
+        uint16_t *c = (uint16_t *)ep.c + z * ep.bsc + (int64_t)row * ep.rsc + (int64_t)col * ep.csc;
+        float v = ep.alpha_f * acc;
+        if (ep.beta_f == 1.0f) {
+            v = bf16_widen(*c) + v;
+        } else if (ep.beta_f != 0.0f) {
+            v = __builtin_fmaf(ep.beta_f, bf16_widen(*c), v);
+        }
+        *c = bf16_rne(v);
+    }
+};
+
+template <>
+struct Store<EpiKind::Q8> {
+    __device__ __forceinline__ static void apply(const EpiParams &ep, int64_t z, int row, int col,
+                                                 int32_t acc) {
+        int ch = ep.axis ? col : row;
+        float s = ep.scales ? ep.scales[ch] : ep.scale;
+        int32_t b = ep.bias ? ep.bias[ch] : 0;
+        int32_t q = requant_value(acc, b, s, ep.zp, ep.lo, ep.hi);
+        uint8_t *c = (uint8_t *)ep.c + z * ep.bsc + (int64_t)row * ep.rsc + (int64_t)col * ep.csc;
+        *c = (uint8_t)(q & 0xFF);
+    }
+};
+
+}  // namespace gk

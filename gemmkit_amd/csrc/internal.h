@@ -1,0 +1,83 @@
+// internal.h -- shared declarations of the gfx950 GEMM engine (not installed).
+//
+// Kernel frame.  Every MFMA launch computes C[M,N] = epi(sum_k A[m,k] * B[n,k])
+// where A (M x K) and B (N x K) are "k-contiguous": element (r, p) of an operand
+// lives at base + r*ld + p, rows 16-byte aligned, K*sizeof(T) a multiple of 16.
+// That is the layout gemmkit's packers produce for its microkernels
+// (src/pack.rs:28-117): the contraction index is the fast one.  The host
+// dispatcher (dispatch.cpp) brings every call into this frame with the
+// reference's orientation swap (src/dispatch.rs:395-417) -- free here because
+// both operands are k-contiguous -- and packs an operand into the workspace
+// only when its own strides are not k-contiguous.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace gk {
+
+enum class InType : int { I8 = 0, BF16 = 1, F32 = 2 };
+enum class EpiKind : int { I32 = 0, F32 = 1, BF16 = 2, Q8 = 3 };
+
+inline size_t in_size(InType t) { return t == InType::I8 ? 1 : (t == InType::BF16 ? 2 : 4); }
+
+// Epilogue parameters, a POD passed by value to the kernels.
+struct EpiParams {
+    EpiKind kind;
+    void *c;               // output base (kernel frame)
+    int64_t rsc, csc;      // output element strides (kernel frame)
+    int64_t bsc;           // batch stride of C in elements
+    int32_t alpha_i, beta_i;
+    float alpha_f, beta_f;
+    // requantization (EpiKind::Q8)
+    float scale;
+    const float *scales;   // per-channel scales or nullptr
+    const int32_t *bias;   // per-channel bias or nullptr
+    int32_t axis;          // 0: channel = kernel row, 1: channel = kernel column
+    int32_t zp, lo, hi;    // zero point and clamp band (ReLU already folded into lo)
+};
+
+struct MmaArgs {
+    const void *a;         // M x K, k-contiguous
+    const void *b;         // N x K, k-contiguous
+    int64_t lda, ldb;      // row strides in elements
+    int64_t bsa, bsb;      // batch strides in elements
+    int32_t M, N, K;       // K in elements
+    int32_t batch;
+};
+
+// Tile shapes instantiated in mfma_gemm.hip.
+enum class Tile : int { T256x256 = 0, T256x128 = 1, T128x128 = 2, T64x64 = 3 };
+
+hipError_t launch_mma(InType in, Tile tile, const MmaArgs &args, const EpiParams &ep,
+                      hipStream_t stream);
+
+// GEMV route (gemv.hip).  Dot form: out[r] = epi(sum_p mat[r,p] * vec_j[p]) for
+// nvec vectors (nvec <= 8); mat rows are k-contiguous.
+struct GemvArgs {
+    const void *mat;       // R x K, k-contiguous rows, ld elements apart
+    int64_t ld;
+    const void *vec;       // nvec x K, k-contiguous, vld apart
+    int64_t vld;
+    int32_t R, K, nvec;
+    // Output element (vector j, matrix row r) is stored as the epilogue's
+    // (row j, column r): at c + j*rsc + r*csc of the EpiParams.
+};
+hipError_t launch_gemv(InType in, const GemvArgs &g, const EpiParams &ep, hipStream_t stream);
+
+// Pack a strided rows x K operand into a k-contiguous buffer with row stride
+// ld (>= K, ld*esize a multiple of 16); columns [K, ld) are zero-filled.
+hipError_t launch_pack(InType in, const void *src, int64_t rs, int64_t cs, int64_t rows,
+                       int64_t K, void *dst, int64_t ld, hipStream_t stream);
+
+// C <- beta*C for the degenerate k == 0 / alpha == 0 cases (scale_c_int,
+// src/dispatch/int.rs:150-163, and its float twin src/dispatch.rs:484-497).
+hipError_t launch_scale_c(EpiKind kind, void *c, int64_t m, int64_t n, int64_t rsc,
+                          int64_t csc, int64_t batch, int64_t bsc, int32_t beta_i,
+                          float beta_f, hipStream_t stream);
+
+// k == 0 requant fill (requant_degenerate, src/dispatch/int.rs:735-752).
+hipError_t launch_requant_fill(const EpiParams &ep, int64_t m, int64_t n, hipStream_t stream);
+
+}  // namespace gk

@@ -1,0 +1,299 @@
+/*
+ * gemmkit_hip.h -- C ABI of the MI355X (gfx950) GEMM engine.
+ *
+ * The entry points mirror gemmkit's public Rust API one for one (the citations
+ * are gemmkit/src/... file:line of the function each one replaces), so a
+ * `-sys` binding can sit behind the same Rust signatures:
+ *   - the checked tier takes strided views with their slice lengths
+ *     (MatRef/MatMut, src/api.rs:92-180) and reproduces the reference's
+ *     validation, returning an error code where the reference panics;
+ *   - the `_unchecked` tier takes raw pointers and element strides, exactly the
+ *     reference's `*_unchecked_with` argument lists (negative strides allowed);
+ *   - every entry takes a `gk_workspace*` first: NULL means the library's own
+ *     per-thread workspace (the reference's thread-local pool,
+ *     src/workspace.rs:225-246), non-NULL is the `_with(&mut Workspace, ..)` twin.
+ *
+ * All matrix pointers are DEVICE pointers (HBM).  By default every call is
+ * synchronous like the reference (C is complete on return); gk_set_synchronous(0)
+ * turns calls into stream-ordered launches on the stream set by gk_set_stream.
+ *
+ * Return value: GK_OK (0) or a negative gk_status; gk_last_error() then holds
+ * the message, worded as the reference's panic message ("gemmkit: ...").
+ * Element strides are in elements, as in the reference.
+ */
+#ifndef GEMMKIT_HIP_H
+#define GEMMKIT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ status */
+
+typedef enum gk_status {
+    GK_OK = 0,
+    GK_ERR_SHAPE = -1,       /* dimension mismatch (reference: assert_eq! panics)      */
+    GK_ERR_VIEW = -2,        /* view out of its slice, negative stride, bad batch stride */
+    GK_ERR_ALIAS = -3,       /* C aliases itself / A / B / bias / scales              */
+    GK_ERR_ARG = -4,         /* scale or zero-point out of range, bad enum value      */
+    GK_ERR_LAYOUT = -5,      /* prepacked-B call with a row-major-ish C               */
+    GK_ERR_OVERFLOW = -6,    /* a size computation overflows                          */
+    GK_ERR_DEVICE = -7,      /* HIP runtime failure or no device                      */
+    GK_ERR_NOMEM = -8        /* device allocation failed                              */
+} gk_status;
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *gk_last_error(void);
+
+/* Library version string. */
+const char *gk_version(void);
+
+/* ---------------------------------------------------------------- runtime */
+
+/* Parallelism request (src/parallel.rs:25): 1 = Serial, 0 = Rayon(0) "all",
+ * n = Rayon(n).  Accepted for drop-in compatibility and ignored: the device
+ * grid decides. */
+typedef uint32_t gk_par;
+#define GK_PAR_SERIAL 1u
+#define GK_PAR_ALL 0u
+
+/* bf16 values travel as their 16-bit patterns. */
+typedef uint16_t gk_bf16;
+
+/* Initialise the HIP device (called lazily by every entry point). */
+int gk_init(void);
+
+/* Stream the calling thread's launches go to (a hipStream_t; NULL = the null
+ * stream).  Thread-local. */
+int gk_set_stream(void *hip_stream);
+void *gk_get_stream(void);
+
+/* 1 (default): every call waits for its kernels, as the reference's synchronous
+ * entry points do.  0: calls only enqueue.  Thread-local. */
+int gk_set_synchronous(int on);
+
+/* Device scratch arena (src/workspace.rs:53): holds packed operands for
+ * layouts the kernels cannot read in place.  Grows on demand, never shrinks. */
+typedef struct gk_workspace gk_workspace;
+gk_workspace *gk_workspace_new(void);
+void gk_workspace_free(gk_workspace *ws);
+size_t gk_workspace_bytes(const gk_workspace *ws);
+
+/* ------------------------------------------------------------------ views */
+
+/* MatRef / MatMut (src/api.rs:92-180): element (i, j) lives at
+ * data + i*rs + j*cs; `len` is the backing slice length in elements. */
+typedef struct gk_mat_ref {
+    const void *data;
+    size_t len;
+    size_t rows;
+    size_t cols;
+    ptrdiff_t rs;
+    ptrdiff_t cs;
+} gk_mat_ref;
+
+typedef struct gk_mat_mut {
+    void *data;
+    size_t len;
+    size_t rows;
+    size_t cols;
+    ptrdiff_t rs;
+    ptrdiff_t cs;
+} gk_mat_mut;
+
+/* --------------------------------------------------------- plain GEMM: f32 */
+
+/* gemm::<f32> / gemm_with (src/api.rs:400, :418): C <- alpha*A*B + beta*C.
+ * beta == 0 never reads C.  m == 1 or n == 1 takes the GEMV route, as
+ * dispatch/float.rs:81 does. */
+int gk_gemm_f32(gk_workspace *ws, float alpha, const gk_mat_ref *a, const gk_mat_ref *b,
+                float beta, const gk_mat_mut *c, gk_par par);
+
+/* gemm_unchecked::<f32> / gemm_unchecked_with (src/api.rs:469, :544). */
+int gk_gemm_f32_unchecked(gk_workspace *ws, size_t m, size_t k, size_t n, float alpha,
+                          const float *a, ptrdiff_t rsa, ptrdiff_t csa,
+                          const float *b, ptrdiff_t rsb, ptrdiff_t csb,
+                          float beta, float *c, ptrdiff_t rsc, ptrdiff_t csc, gk_par par);
+
+/* -------------------------------------------------------- plain GEMM: bf16 */
+
+/* gemm::<bf16> (src/api.rs:400 with GemmScalar for bf16, src/dispatch/mixed.rs:1395):
+ * bf16 inputs, f32 accumulation, alpha*acc + beta*C in f32, one RNE narrowing to
+ * bf16 (NaN -> (bits>>16)|0x40).  alpha/beta are bf16 like the reference's. */
+int gk_gemm_bf16(gk_workspace *ws, gk_bf16 alpha, const gk_mat_ref *a, const gk_mat_ref *b,
+                 gk_bf16 beta, const gk_mat_mut *c, gk_par par);
+int gk_gemm_bf16_unchecked(gk_workspace *ws, size_t m, size_t k, size_t n, gk_bf16 alpha,
+                           const gk_bf16 *a, ptrdiff_t rsa, ptrdiff_t csa,
+                           const gk_bf16 *b, ptrdiff_t rsb, ptrdiff_t csb,
+                           gk_bf16 beta, gk_bf16 *c, ptrdiff_t rsc, ptrdiff_t csc, gk_par par);
+
+/* Extension (no reference counterpart; the reference's bf16 GEMM always
+ * narrows): bf16 inputs, f32 accumulation, f32 alpha/beta and f32 output C.
+ * Same validation as gemm::<bf16>. */
+int gk_gemm_bf16_f32out(gk_workspace *ws, float alpha, const gk_mat_ref *a,
+                        const gk_mat_ref *b, float beta, const gk_mat_mut *c, gk_par par);
+int gk_gemm_bf16_f32out_unchecked(gk_workspace *ws, size_t m, size_t k, size_t n, float alpha,
+                                  const gk_bf16 *a, ptrdiff_t rsa, ptrdiff_t csa,
+                                  const gk_bf16 *b, ptrdiff_t rsb, ptrdiff_t csb,
+                                  float beta, float *c, ptrdiff_t rsc, ptrdiff_t csc,
+                                  gk_par par);
+
+/* ------------------------------------------------------------- i8 -> i32 */
+
+/* gemm_i8 / gemm_i8_with (src/api/int8.rs:22, :38): i8 inputs, i32 alpha/beta/C,
+ * all arithmetic wrapping i32. */
+int gk_gemm_i8(gk_workspace *ws, int32_t alpha, const gk_mat_ref *a, const gk_mat_ref *b,
+               int32_t beta, const gk_mat_mut *c, gk_par par);
+
+/* gemm_i8_unchecked / gemm_i8_unchecked_with (src/api/int8.rs:86, :136). */
+int gk_gemm_i8_unchecked(gk_workspace *ws, size_t m, size_t k, size_t n, int32_t alpha,
+                         const int8_t *a, ptrdiff_t rsa, ptrdiff_t csa,
+                         const int8_t *b, ptrdiff_t rsb, ptrdiff_t csb,
+                         int32_t beta, int32_t *c, ptrdiff_t rsc, ptrdiff_t csc, gk_par par);
+
+/* --------------------------------------------------------- requantization */
+
+/* Channel axis of a requant scale vector / bias.  GK_AXIS_ROW is the
+ * reference's only choice (RequantScale::PerRow, Requantize::bias, length m,
+ * src/api/int8.rs:185-209); GK_AXIS_COL (length n, per output column) is an
+ * extension of this engine. */
+#define GK_AXIS_ROW 0
+#define GK_AXIS_COL 1
+
+/* Activation after requantization.  GK_ACT_RELU is an extension: it clamps the
+ * quantized value below at max(LO, zero_point), which equals quantizing
+ * max(0, real value) because round-half-even is monotone with rne(0) = 0. */
+#define GK_ACT_NONE 0
+#define GK_ACT_RELU 1
+
+/* Requantize (src/api/int8.rs:185-209) plus the two extension fields.
+ * scales == NULL selects RequantScale::PerTensor(scale); otherwise `scales`
+ * (device, scales_len entries) is the per-channel vector.  bias == NULL means
+ * no bias.  Output: clamp(zp + round_half_even(scale*(acc + bias)), LO, HI). */
+typedef struct gk_requantize {
+    float scale;
+    const float *scales;
+    size_t scales_len;
+    int32_t zero_point;
+    const int32_t *bias;
+    size_t bias_len;
+    int32_t axis; /* GK_AXIS_ROW or GK_AXIS_COL */
+    int32_t act;  /* GK_ACT_NONE or GK_ACT_RELU  */
+} gk_requantize;
+
+/* gemm_i8_requant / _with (src/api/int8.rs:230, :280): i8 output, LO/HI = -128/127. */
+int gk_gemm_i8_requant(gk_workspace *ws, const gk_mat_ref *a, const gk_mat_ref *b,
+                       const gk_requantize *req, const gk_mat_mut *c, gk_par par);
+
+/* gemm_i8_requant_u8 / _with (src/api/int8.rs:479, :510): u8 output, LO/HI = 0/255. */
+int gk_gemm_i8_requant_u8(gk_workspace *ws, const gk_mat_ref *a, const gk_mat_ref *b,
+                          const gk_requantize *req, const gk_mat_mut *c, gk_par par);
+
+/* gemm_i8_requant_unchecked(_with) (src/api/int8.rs:347, :410) and the u8 twins
+ * (:562, :615), with the axis/act extension arguments appended (pass
+ * GK_AXIS_ROW, GK_ACT_NONE for the reference's behaviour). */
+int gk_gemm_i8_requant_unchecked(gk_workspace *ws, size_t m, size_t k, size_t n,
+                                 const int8_t *a, ptrdiff_t rsa, ptrdiff_t csa,
+                                 const int8_t *b, ptrdiff_t rsb, ptrdiff_t csb,
+                                 float scale, const float *row_scales, uint8_t has_row_scales,
+                                 int32_t zero_point, const int32_t *bias, uint8_t has_bias,
+                                 int8_t *c, ptrdiff_t rsc, ptrdiff_t csc, gk_par par,
+                                 int32_t axis, int32_t act);
+int gk_gemm_i8_requant_u8_unchecked(gk_workspace *ws, size_t m, size_t k, size_t n,
+                                    const int8_t *a, ptrdiff_t rsa, ptrdiff_t csa,
+                                    const int8_t *b, ptrdiff_t rsb, ptrdiff_t csb,
+                                    float scale, const float *row_scales,
+                                    uint8_t has_row_scales, int32_t zero_point,
+                                    const int32_t *bias, uint8_t has_bias,
+                                    uint8_t *c, ptrdiff_t rsc, ptrdiff_t csc, gk_par par,
+                                    int32_t axis, int32_t act);
+
+/* -------------------------------------------------------- prepacked i8 RHS */
+
+/* PackedRhs<i8> (src/api/packed.rs:34-52): an opaque, read-only device copy of
+ * B in the kernels' k-contiguous tile layout; it can be shared by concurrent
+ * calls and is released with gk_packed_rhs_free. */
+typedef struct gk_packed_rhs gk_packed_rhs;
+
+/* prepack_rhs_i8 (src/api/packed.rs:372): B is a device view (k x n). */
+int gk_prepack_rhs_i8(const gk_mat_ref *b, gk_packed_rhs **out);
+/* prepack_rhs_i8_unchecked (src/api/packed.rs:406). */
+int gk_prepack_rhs_i8_unchecked(const int8_t *b, ptrdiff_t rsb, ptrdiff_t csb, size_t k,
+                                size_t n, gk_packed_rhs **out);
+void gk_packed_rhs_free(gk_packed_rhs *p);
+/* PackedRhs::rows / cols (src/api/packed.rs:43-51). */
+size_t gk_packed_rhs_rows(const gk_packed_rhs *p);
+size_t gk_packed_rhs_cols(const gk_packed_rhs *p);
+
+/* gemm_i8_packed_b / _with (src/api/packed.rs:473, :494): bit-identical to
+ * gemm_i8; like the reference it requires a column-major-ish C
+ * (|csc| >= |rsc|). */
+int gk_gemm_i8_packed_b(gk_workspace *ws, int32_t alpha, const gk_mat_ref *a,
+                        const gk_packed_rhs *packed, int32_t beta, const gk_mat_mut *c,
+                        gk_par par);
+/* gemm_i8_packed_b_unchecked(_with) (src/api/packed.rs:575, :612). */
+int gk_gemm_i8_packed_b_unchecked(gk_workspace *ws, int32_t alpha, size_t m, const int8_t *a,
+                                  ptrdiff_t rsa, ptrdiff_t csa, const gk_packed_rhs *packed,
+                                  int32_t beta, int32_t *c, ptrdiff_t rsc, ptrdiff_t csc,
+                                  gk_par par);
+
+/* Extension (the reference has no prepacked requant entry): requantizing GEMM
+ * against a prepacked B, i8 or u8 output, any C orientation.  Validation as
+ * gk_gemm_i8_requant with B's shape taken from `packed`. */
+int gk_gemm_i8_packed_b_requant(gk_workspace *ws, const gk_mat_ref *a,
+                                const gk_packed_rhs *packed, const gk_requantize *req,
+                                const gk_mat_mut *c, gk_par par);
+int gk_gemm_i8_packed_b_requant_u8(gk_workspace *ws, const gk_mat_ref *a,
+                                   const gk_packed_rhs *packed, const gk_requantize *req,
+                                   const gk_mat_mut *c, gk_par par);
+
+/* ----------------------------------------------------------- batched GEMM */
+
+/* gemm_batched::<f32> / _with (src/api/batched.rs:188, :225): element bi uses
+ * A + bi*a_bs, B + bi*b_bs, C + bi*c_bs (element strides; 0 broadcasts A or B). */
+int gk_gemm_batched_f32(gk_workspace *ws, size_t batch, float alpha,
+                        const gk_mat_ref *a, ptrdiff_t a_bs,
+                        const gk_mat_ref *b, ptrdiff_t b_bs, float beta,
+                        const gk_mat_mut *c, ptrdiff_t c_bs, gk_par par);
+/* gemm_batched_unchecked(_with) (src/api/batched.rs:594, :649). */
+int gk_gemm_batched_f32_unchecked(gk_workspace *ws, size_t batch, size_t m, size_t k,
+                                  size_t n, float alpha,
+                                  const float *a, ptrdiff_t rsa, ptrdiff_t csa, ptrdiff_t a_bs,
+                                  const float *b, ptrdiff_t rsb, ptrdiff_t csb, ptrdiff_t b_bs,
+                                  float beta, float *c, ptrdiff_t rsc, ptrdiff_t csc,
+                                  ptrdiff_t c_bs, gk_par par);
+
+/* gemm_batched::<bf16> (src/api/batched.rs:188): bf16 in and out. */
+int gk_gemm_batched_bf16(gk_workspace *ws, size_t batch, gk_bf16 alpha,
+                         const gk_mat_ref *a, ptrdiff_t a_bs,
+                         const gk_mat_ref *b, ptrdiff_t b_bs, gk_bf16 beta,
+                         const gk_mat_mut *c, ptrdiff_t c_bs, gk_par par);
+int gk_gemm_batched_bf16_unchecked(gk_workspace *ws, size_t batch, size_t m, size_t k,
+                                   size_t n, gk_bf16 alpha,
+                                   const gk_bf16 *a, ptrdiff_t rsa, ptrdiff_t csa,
+                                   ptrdiff_t a_bs, const gk_bf16 *b, ptrdiff_t rsb,
+                                   ptrdiff_t csb, ptrdiff_t b_bs, gk_bf16 beta, gk_bf16 *c,
+                                   ptrdiff_t rsc, ptrdiff_t csc, ptrdiff_t c_bs, gk_par par);
+
+/* Extension: batched bf16 x bf16 with f32 accumulation and f32 alpha/beta/C
+ * (the attention-score shape); validation as gemm_batched. */
+int gk_gemm_batched_bf16_f32out(gk_workspace *ws, size_t batch, float alpha,
+                                const gk_mat_ref *a, ptrdiff_t a_bs,
+                                const gk_mat_ref *b, ptrdiff_t b_bs, float beta,
+                                const gk_mat_mut *c, ptrdiff_t c_bs, gk_par par);
+int gk_gemm_batched_bf16_f32out_unchecked(gk_workspace *ws, size_t batch, size_t m, size_t k,
+                                          size_t n, float alpha,
+                                          const gk_bf16 *a, ptrdiff_t rsa, ptrdiff_t csa,
+                                          ptrdiff_t a_bs, const gk_bf16 *b, ptrdiff_t rsb,
+                                          ptrdiff_t csb, ptrdiff_t b_bs, float beta, float *c,
+                                          ptrdiff_t rsc, ptrdiff_t csc, ptrdiff_t c_bs,
+                                          gk_par par);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* GEMMKIT_HIP_H */
