@@ -84,6 +84,9 @@ def set_synchronous(on: bool) -> None:
 
 def _bind_stream() -> None:
     L = _lib.lib()
+    if not torch.cuda.is_available():
+        raise GemmkitError(-7, "gemmkit_amd: no HIP device available; tensors must live on "
+                               "the HIP device")
     s = torch.cuda.current_stream().cuda_stream
     L.gk_set_stream(C.c_void_p(s))
 

@@ -81,6 +81,9 @@ def _oracle() -> C.CDLL:
                                            C.c_float, _f32p, C.c_int32, _i32p, C.c_int,
                                            C.c_int32, C.c_int32, _u8p, _sd, _sd]
         lib.or_gemm_i8_requant.restype = None
+        lib.or_requant_map.argtypes = [_sz, _sz, _i32p, _sd, _sd, C.c_float, _f32p, C.c_int32,
+                                       _i32p, C.c_int, C.c_int32, C.c_int32, _u8p, _sd, _sd]
+        lib.or_requant_map.restype = None
         lib.or_bf16_from_f32.argtypes = [C.c_float]
         lib.or_bf16_from_f32.restype = C.c_uint16
         lib.or_bf16_from_f32_n.argtypes = [_f32p, _sz, _u16p]
@@ -176,6 +179,15 @@ def gemm_i8_requant(m, k, n, a, rsa, csa, b, rsb, csb, scale, scales, zp, bias, 
     lib.or_gemm_i8_requant(m, k, n, _ptr(a, _i8p), rsa, csa, _ptr(b, _i8p), rsb, csb,
                            float(scale), sp, int(zp), bp, int(axis), int(lo), int(hi),
                            C.cast(c.ctypes.data, _u8p), rsc, csc)
+
+
+def requant_map(m, n, acc, ra, ca, scale, scales, zp, bias, axis, lo, hi, c, rc, cc) -> None:
+    """Requant map over an existing i32 accumulator matrix into byte buffer ``c``."""
+    sp = _ptr(np.ascontiguousarray(scales, np.float32), _f32p) if scales is not None else None
+    bp = _ptr(np.ascontiguousarray(bias, np.int32), _i32p) if bias is not None else None
+    keep = (scales, bias)  # noqa: F841
+    _oracle().or_requant_map(m, n, _ptr(acc, _i32p), ra, ca, float(scale), sp, int(zp), bp,
+                             int(axis), int(lo), int(hi), C.cast(c.ctypes.data, _u8p), rc, cc)
 
 
 def bf16_bits(x: np.ndarray) -> np.ndarray:

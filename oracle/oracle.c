@@ -219,6 +219,25 @@ OR_API void or_gemm_i8_requant(size_t m, size_t k, size_t n,
     }
 }
 
+/* The requant map applied to an existing i32 accumulator matrix (acc given
+ * at strides ra/ca, bytes written at rc/cc): the same per-element map as
+ * or_gemm_i8_requant, for checking a requantizing GEMM against a separately
+ * checked i32 GEMM of the same operands. */
+OR_API void or_requant_map(size_t m, size_t n, const int32_t *acc, ptrdiff_t ra, ptrdiff_t ca,
+                           float scale, const float *scales, int32_t zp, const int32_t *bias,
+                           int axis, int32_t lo, int32_t hi, uint8_t *c, ptrdiff_t rc,
+                           ptrdiff_t cc) {
+    #pragma omp parallel for schedule(static) if (m * n > (1u << 20))
+    for (ptrdiff_t i = 0; i < (ptrdiff_t)m; ++i)
+        for (size_t j = 0; j < n; ++j) {
+            size_t ch = axis ? j : (size_t)i;
+            float s = scales ? scales[ch] : scale;
+            int32_t bb = bias ? bias[ch] : 0;
+            int32_t q = or_requant_one(acc[i * ra + (ptrdiff_t)j * ca], bb, s, zp, lo, hi);
+            c[i * rc + (ptrdiff_t)j * cc] = (uint8_t)(q & 0xFF);
+        }
+}
+
 /* --------------------------------------------------------------------- bf16 */
 
 /* f32 -> bf16 bits, round-to-nearest-even; NaN becomes (bits >> 16) | 0x0040.

@@ -1,0 +1,240 @@
+"""CPU tests that pin the oracle before anything is compared against it.
+
+Each oracle function is checked against something that does not share its
+code: the reference's literal known answers, fixtures written by pure-Python
+models (tests/golden/make_golden.py), numpy's exact int64 / float64
+arithmetic, torch's RNE bf16 conversion, brute force on tiny inputs, and the
+ABFT checksum identity.  Planted-mistake checks confirm the comparisons would
+catch a dropped term or a transposed operand.
+"""
+import json
+import os
+import struct
+
+import numpy as np
+import pytest
+
+import oracle
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def load(name):
+    with open(os.path.join(GOLD, name)) as f:
+        return json.load(f)
+
+
+# ------------------------------------------------------------------- i8 GEMM
+
+def test_i8_small_fixtures():
+    for case in load("i8_gemm_small.json"):
+        m, k, n = case["m"], case["k"], case["n"]
+        a = np.array(case["a"], np.int8)
+        b = np.array(case["b"], np.int8)
+        c = np.array(case["c0"], np.int32)
+        oracle.gemm_i8(m, k, n, case["alpha"], a, k, 1, b, n, 1, case["beta"], c, n, 1)
+        assert c.tolist() == case["expected"], (m, k, n, case["alpha"], case["beta"])
+
+
+def test_i8_generator_matches_fixture_inputs():
+    case = load("i8_gemm_small.json")[2]
+    m, k = case["m"], case["k"]
+    assert oracle.rand_i8_100(0x100 + m * 7 + k, m * k).tolist() == case["a"]
+
+
+def test_i8_wrap_kat():
+    kat = load("kats.json")["i8_wrap"]
+    a = np.array(kat["a"], np.int8)
+    b = np.array(kat["b"], np.int8)
+    c = np.array(kat["c0"], np.int32)
+    oracle.gemm_i8(2, 2, 2, kat["alpha"], a, 2, 1, b, 2, 1, kat["beta"], c, 2, 1)
+    acc = 127 * 127 * 2
+    wrap = lambda v: (v + 2**31) % 2**32 - 2**31  # noqa: E731
+    assert c.tolist() == [wrap(x + wrap(kat["alpha"] * acc)) for x in kat["c0"]]
+
+
+@pytest.mark.parametrize("m,k,n", [(5, 9, 4), (64, 200, 33), (130, 1000, 70)])
+def test_i8_vs_numpy_int64_all_layouts(m, k, n):
+    a = oracle.rng_i8_full(m, m * k).reshape(m, k)
+    b = oracle.rng_i8_full(n, k * n).reshape(k, n)
+    ref = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.int32)
+    for (rsa, csa, at) in ((k, 1, a), (1, m, a.T)):
+        for (rsb, csb, bt) in ((n, 1, b), (1, k, b.T)):
+            for (rsc, csc) in ((n, 1), (1, m)):
+                c = np.zeros(m * n, np.int32)
+                oracle.gemm_i8(m, k, n, 1, np.ascontiguousarray(at).ravel(), rsa, csa,
+                               np.ascontiguousarray(bt).ravel(), rsb, csb, 0, c, rsc, csc)
+                got = c.reshape(m, n) if rsc == n else c.reshape(n, m).T
+                assert np.array_equal(got, ref)
+
+
+def test_i8_abft_identity_and_planted_transpose():
+    m, k, n = 40, 50, 30
+    a = oracle.rng_i8_full(3, m * k)
+    b = oracle.rng_i8_full(4, k * n)
+    c = np.zeros(m * n, np.int32)
+    oracle.gemm_i8(m, k, n, 1, a, k, 1, b, n, 1, 0, c, n, 1)
+    assert np.array_equal(oracle.colsum_i32(m, n, c, n, 1), oracle.abft_i8(m, k, n, a, k, 1, b, n, 1))
+    # a transposed operand (B read column-major by mistake) must break the identity
+    bad = np.zeros(m * n, np.int32)
+    kk = min(k, n)
+    oracle.gemm_i8(m, kk, kk, 1, a, k, 1, b, 1, n, 0, bad, kk, 1)
+    good = np.zeros(m * kk, np.int32)
+    oracle.gemm_i8(m, kk, kk, 1, a, k, 1, b, n, 1, 0, good, kk, 1)
+    assert not np.array_equal(bad[:m * kk], good)
+
+
+def test_i8_negative_strides():
+    m, k, n = 12, 9, 7
+    a = oracle.rand_i8_100(5, m * k)
+    b = oracle.rand_i8_100(6, k * n)
+    fwd = np.zeros(m * n, np.int32)
+    oracle.gemm_i8(m, k, n, 1, a, k, 1, b, n, 1, 0, fwd, n, 1)
+    rev = np.zeros(m * n, np.int32)
+    oracle.gemm_i8(m, k, n, 1, a, -k, 1, b, n, 1, 0, rev, n, 1, a_off=(m - 1) * k)
+    assert np.array_equal(rev.reshape(m, n), fwd.reshape(m, n)[::-1])
+
+
+# ------------------------------------------------------------------- requant
+
+def test_requant_store_sweep_fixture():
+    sw = load("requant_store_sweep.json")
+    accs = sw["accumulators"]
+    assert len(accs) == 104
+    for case in sw["cases"]:
+        s = struct.unpack("<f", struct.pack("<I", case["scale_f32_bits"]))[0]
+        got = [oracle.requant_one(v, 0, s, case["zp"], case["lo"], case["hi"]) & 0xFF for v in accs]
+        assert got == case["expected_low_byte"], case["scale_f32_bits"]
+
+
+def test_requant_ties_kat():
+    kat = load("kats.json")["requant_ties"]
+    assert [oracle.requant_one(v, 0, kat["scale"], kat["zp"]) for v in kat["a"]] == kat["expected"]
+
+
+def test_requant_bias_wraps_and_round_ne():
+    # wrapping bias add (src/kernel/epilogue.rs:825): MAX + 1 wraps to MIN
+    assert oracle.requant_one(2**31 - 1, 1, 1.0, 0) == -128
+    assert oracle.requant_one(-2**31, -1, 1.0, 0) == 127
+    # the 2^52 trick equals round-half-even, and passes large values through
+    for x in (0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 4503599627370495.5, 1e300, -1e300, 0.49999999999999994):
+        assert oracle.round_ne_f64(x) == (round(x) if abs(x) < 2**52 else x)
+    # a planted round-half-up map would give 3 here; the fixture and the
+    # oracle both say 2 (ties to even)
+    planted = int(np.floor(5 * 0.5 + 0.5))
+    assert planted == 3 and oracle.requant_one(5, 0, 0.5, 0) == 2
+
+
+def test_requant_gemm_composition_vs_python():
+    m, k, n = 9, 33, 11
+    a = oracle.rng_i8_sym127(1, m * k)
+    b = oracle.rng_i8_sym127(2, k * n)
+    scales = np.array([0.003, 0.5, 1.0, 7.25, 0.0078125, 0.1, 0.01, 0.02, 0.3], np.float32)
+    bias = np.array([(i * 977) % 2001 - 1000 for i in range(m)], np.int32)
+    out = np.zeros(m * n, np.int8)
+    oracle.gemm_i8_requant(m, k, n, a, k, 1, b, n, 1, 0.0, scales, 3, bias, 0, -128, 127,
+                           out, n, 1)
+    acc = a.reshape(m, k).astype(np.int64) @ b.reshape(k, n).astype(np.int64)
+    for i in range(m):
+        for j in range(n):
+            x = float(int(acc[i, j]) + int(bias[i])) * float(scales[i])
+            q = max(-128, min(127, round(x) + 3))
+            assert out[i * n + j] == q
+    # per-column axis: channel index follows j
+    outc = np.zeros(m * n, np.uint8)
+    sc = np.linspace(0.001, 0.05, n).astype(np.float32)
+    oracle.gemm_i8_requant(m, k, n, a, k, 1, b, n, 1, 0.0, sc, 10, None, 1, 0, 255, outc, n, 1)
+    for i in range(m):
+        for j in range(n):
+            q = max(0, min(255, round(float(int(acc[i, j])) * float(sc[j])) + 10))
+            assert outc[i * n + j] == q
+
+
+def test_requant_map_equals_fused():
+    m, k, n = 20, 64, 17
+    a = oracle.rng_i8_sym127(5, m * k)
+    b = oracle.rng_i8_sym127(6, k * n)
+    sc = np.linspace(0.001, 0.02, n).astype(np.float32)
+    bias = np.arange(n, dtype=np.int32) * 1000 - 8000
+    fused = np.zeros(m * n, np.int8)
+    oracle.gemm_i8_requant(m, k, n, a, k, 1, b, n, 1, 0.0, sc, 0, bias, 1, 0, 127, fused, n, 1)
+    acc = np.zeros(m * n, np.int32)
+    oracle.gemm_i8(m, k, n, 1, a, k, 1, b, n, 1, 0, acc, n, 1)
+    mapped = np.zeros(m * n, np.int8)
+    oracle.requant_map(m, n, acc, n, 1, 0.0, sc, 0, bias, 1, 0, 127, mapped, n, 1)
+    assert np.array_equal(fused, mapped)
+
+
+# ---------------------------------------------------------------------- bf16
+
+def test_bf16_rne_vs_torch():
+    import torch
+    x = np.concatenate([oracle.rng_normal(1, 20000) * 10.0 ** np.arange(-20, 20, 2).repeat(1000),
+                        np.array([0.0, -0.0, 1.0, 65504.0, 3.4e38, -3.4e38, 1e-40, np.inf, -np.inf])])
+    x = x.astype(np.float32)
+    # exact ties: 1 + 2^-8 (tie, round to even 1.0) and 1 + 3*2^-8 (tie, round up)
+    ties = np.array([1 + 2.0 ** -8, 1 + 3 * 2.0 ** -8, -(1 + 2.0 ** -8)], np.float32)
+    x = np.concatenate([x, ties])
+    got = oracle.bf16_bits(x)
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+    assert got[-3] == 0x3F80 and got[-2] == 0x3F82 and got[-1] == 0xBF80
+
+
+def test_bf16_nan_rule():
+    # NaN keeps its upper bits and is quieted: (bits >> 16) | 0x40
+    for bits in (0x7F800001, 0x7FC00000, 0xFF812345, 0x7FFFFFFF):
+        f = np.array([bits], np.uint32).view(np.float32)
+        assert oracle.bf16_bits(f)[0] == ((bits >> 16) | 0x40)
+
+
+# ----------------------------------------------------------------- f64 GEMM
+
+def test_readme_kat_f64():
+    kat = load("kats.json")["readme_2x2"]
+    out = oracle.gemm_f64(2, 3, 2, 1.0, np.array(kat["a"], np.float32), 3, 1,
+                          np.array(kat["b"], np.float32), 2, 1)
+    assert out.ravel().tolist() == kat["expected"]
+
+
+def test_f64_gemm_and_gemv_vs_numpy():
+    m, k, n = 37, 50, 23
+    a = oracle.rand_vec(1, m * k).astype(np.float32)
+    b = oracle.rand_vec(2, k * n).astype(np.float32)
+    c0 = oracle.rand_vec(3, m * n).astype(np.float32)
+    got = oracle.gemm_f64(m, k, n, 0.5, a, k, 1, b, n, 1, -2.0, c0, n, 1)
+    ref = 0.5 * (a.reshape(m, k).astype(np.float64) @ b.reshape(k, n).astype(np.float64)) \
+        - 2.0 * c0.reshape(m, n).astype(np.float64)
+    assert np.allclose(got, ref, rtol=1e-12, atol=1e-12)
+    # beta == 0 never reads C: NaN in C0 must not leak
+    nan_c = np.full(m * n, np.nan, np.float32)
+    assert np.isfinite(oracle.gemm_f64(m, k, n, 1.0, a, k, 1, b, n, 1, 0.0, nan_c, n, 1)).all()
+    y = oracle.gemv_f64(m, k, 1.0, a, k, 1, b[:k], 1)
+    assert np.allclose(y, a.reshape(m, k).astype(np.float64) @ b[:k].astype(np.float64))
+
+
+# ------------------------------------------------------------------ CPU port
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (33, 17, 19), (100, 300, 50), (257, 1024, 129)])
+@pytest.mark.parametrize("alpha,beta", [(1, 0), (3, -2), (1, 1)])
+@pytest.mark.parametrize("row_major_c", [True, False])
+def test_cpu_port_bit_exact(m, k, n, alpha, beta, row_major_c):
+    a = oracle.rng_i8_full(10 + m, m * k)
+    b = oracle.rng_i8_full(20 + n, k * n)
+    rsc, csc = (n, 1) if row_major_c else (1, m)
+    c0 = ((np.arange(m * n) % 7) - 3).astype(np.int32)
+    want = c0.copy()
+    oracle.gemm_i8(m, k, n, alpha, a, k, 1, b, 1, k, beta, want, rsc, csc)
+    got = c0.copy()
+    oracle.port_gemm_i8(m, k, n, alpha, a, k, 1, b, 1, k, beta, got, rsc, csc, threads=2)
+    assert np.array_equal(got, want)
+
+
+def test_generators_are_reproducible():
+    assert oracle.rng_next_u64(7, 3) == oracle.rng_next_u64(7, 3)
+    x = oracle.rng_i8_full(5, 100000)
+    assert x.min() == -128 and x.max() == 127
+    y = oracle.rng_i8_sym127(5, 100000)
+    assert y.min() == -127 and y.max() == 127
+    u = oracle.rng_unit(5, 100000)
+    assert -1 <= u.min() and u.max() < 1
