@@ -315,6 +315,8 @@ Tile env_tile(bool *forced) {
     if (!s) return Tile::T256x256;
     *forced = true;
     if (!strcmp(s, "256x256")) return Tile::T256x256;
+    if (!strcmp(s, "256x256w8")) return Tile::T256x256w8;
+    if (!strcmp(s, "256x128o2")) return Tile::T256x128o2;
     if (!strcmp(s, "256x128")) return Tile::T256x128;
     if (!strcmp(s, "128x128")) return Tile::T128x128;
     if (!strcmp(s, "64x64")) return Tile::T64x64;
@@ -421,6 +423,13 @@ int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t
         return finish("gemv");
     }
 
+    // Whole 4-element output chunks can go out as one vector access when C is
+    // unit-stride along the kernel's columns and every chunk start is aligned.
+    {
+        const int64_t osz = ep.kind == EpiKind::Q8 ? 1 : (ep.kind == EpiKind::BF16 ? 2 : 4);
+        ep.vec4 = ep.csc == 1 && (M == 1 || ep.rsc % 4 == 0) && (batch <= 1 || bsc % 4 == 0) &&
+                  ((uintptr_t)c % (uintptr_t)(4 * osz)) == 0;
+    }
     MmaArgs args{};
     args.a = A.p;
     args.b = Bt.p;

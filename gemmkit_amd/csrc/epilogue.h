@@ -111,4 +111,71 @@ struct Store<EpiKind::Q8> {
     }
 };
 
+
+// Four consecutive output columns (col .. col+3) of one row, from the
+// LDS-staged accumulators.  `vec` (uniform) says C is unit-stride along columns
+// and 4-element aligned, so whole chunks take one vector access; otherwise, and
+// for chunks that straddle the matrix edge, each element goes through Store.
+template <EpiKind K, typename A>
+__device__ __forceinline__ void store4(const EpiParams &ep, int64_t z, int row, int col, int ncols,
+                                       const A v[4]) {
+    const int nvalid = ncols - col < 4 ? ncols - col : 4;
+    if (!ep.vec4 || nvalid < 4) {
+        for (int e = 0; e < nvalid; ++e) Store<K>::apply(ep, z, row, col + e, v[e]);
+        return;
+    }
+    const int64_t off = z * ep.bsc + (int64_t)row * ep.rsc + col;
+    if constexpr (K == EpiKind::I32) {
+        typedef int v4i_e __attribute__((ext_vector_type(4)));
+        v4i_e *c = (v4i_e *)((int32_t *)ep.c + off);
+        v4i_e o;
+        for (int e = 0; e < 4; ++e) o[e] = (int32_t)((uint32_t)ep.alpha_i * (uint32_t)v[e]);
+        if (ep.beta_i != 0) {
+            v4i_e old = *c;
+            for (int e = 0; e < 4; ++e)
+                o[e] = (int32_t)((ep.beta_i == 1 ? (uint32_t)old[e]
+                                                 : (uint32_t)ep.beta_i * (uint32_t)old[e]) +
+                                 (uint32_t)o[e]);
+        }
+        __builtin_nontemporal_store(o, c);
+    } else if constexpr (K == EpiKind::F32) {
+        typedef float v4f_e __attribute__((ext_vector_type(4)));
+        v4f_e *c = (v4f_e *)((float *)ep.c + off);
+        v4f_e o;
+        for (int e = 0; e < 4; ++e) o[e] = ep.alpha_f * v[e];
+        if (ep.beta_f != 0.0f) {
+            v4f_e old = *c;
+            for (int e = 0; e < 4; ++e)
+                o[e] = ep.beta_f == 1.0f ? old[e] + o[e] : __builtin_fmaf(ep.beta_f, old[e], o[e]);
+        }
+        __builtin_nontemporal_store(o, c);
+    } else if constexpr (K == EpiKind::BF16) {
+        typedef uint32_t v2u_e __attribute__((ext_vector_type(2)));
+        v2u_e *c = (v2u_e *)((uint16_t *)ep.c + off);
+        float f[4];
+        for (int e = 0; e < 4; ++e) f[e] = ep.alpha_f * v[e];
+        if (ep.beta_f != 0.0f) {
+            v2u_e old = *c;
+            for (int e = 0; e < 4; ++e) {
+                float w = bf16_widen((uint16_t)(old[e >> 1] >> (16 * (e & 1))));
+                f[e] = ep.beta_f == 1.0f ? w + f[e] : __builtin_fmaf(ep.beta_f, w, f[e]);
+            }
+        }
+        v2u_e o;
+        o[0] = (uint32_t)bf16_rne(f[0]) | ((uint32_t)bf16_rne(f[1]) << 16);
+        o[1] = (uint32_t)bf16_rne(f[2]) | ((uint32_t)bf16_rne(f[3]) << 16);
+        *c = o;
+    } else {
+        uint32_t word = 0;
+        for (int e = 0; e < 4; ++e) {
+            int ch = ep.axis ? col + e : row;
+            float sc = ep.scales ? ep.scales[ch] : ep.scale;
+            int32_t b = ep.bias ? ep.bias[ch] : 0;
+            int32_t q = requant_value(v[e], b, sc, ep.zp, ep.lo, ep.hi);
+            word |= (uint32_t)(q & 0xFF) << (8 * e);
+        }
+        *(uint32_t *)((uint8_t *)ep.c + off) = word;
+    }
+}
+
 }  // namespace gk

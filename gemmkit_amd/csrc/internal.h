@@ -36,6 +36,7 @@ struct EpiParams {
     const int32_t *bias;   // per-channel bias or nullptr
     int32_t axis;          // 0: channel = kernel row, 1: channel = kernel column
     int32_t zp, lo, hi;    // zero point and clamp band (ReLU already folded into lo)
+    int32_t vec4;          // C is unit-stride along columns and 4-element aligned
 };
 
 struct MmaArgs {
@@ -48,7 +49,14 @@ struct MmaArgs {
 };
 
 // Tile shapes instantiated in mfma_gemm.hip.
-enum class Tile : int { T256x256 = 0, T256x128 = 1, T128x128 = 2, T64x64 = 3 };
+enum class Tile : int {
+    T256x256 = 0,
+    T256x128 = 1,
+    T128x128 = 2,
+    T64x64 = 3,
+    T256x256w8 = 4,
+    T256x128o2 = 5,  // 3-stage ring: two workgroups per CU
+};
 
 hipError_t launch_mma(InType in, Tile tile, const MmaArgs &args, const EpiParams &ep,
                       hipStream_t stream);

@@ -5,22 +5,23 @@
 // (src/driver.rs:402-944, src/kernel/int.rs:138-490, src/kernel/mixed.rs:31-400,
 // src/kernel/float.rs:150-281) with one workgroup per BM x BN output tile.
 //
-// Data path (one workgroup = 4 waves of 64 lanes, 2 x 2 over the tile):
-//   * K advances in stages of 128 bytes per row (128 i8, 64 bf16, 32 f32).
-//   * Each thread loads whole 16-byte chunks of the A and B stage (8 chunks per
-//     row, consecutive threads cover consecutive chunks of a row: coalesced),
-//     and writes them to a double-buffered LDS tile.  Row r of a stage stores
-//     chunk c at slot c ^ (r & 7), so the MFMA operand reads below -- 8 lanes
-//     reading the same chunk of 8 consecutive rows -- hit 8 distinct 16-byte
-//     bank groups (no LDS bank conflicts).
+// Data path (one workgroup = 4 or 8 waves of 64 lanes over one tile):
+//   * K advances in stages of 64 bytes per row (64 i8, 32 bf16, 16 f32).  The
+//     stage's A and B rows go global -> LDS with direct-to-LDS loads
+//     (global_load_lds_dwordx4: lane l of an instruction fills LDS bytes
+//     base + 16*l), into a ring of NS stages, so no VGPRs stage the operands.
+//     Row r of a stage stores its chunk c (16 bytes) in slot c ^ swz(r), which
+//     keeps the operand reads below free of LDS bank conflicts.
 //   * Every MFMA operand is 16 bytes per lane: lane l reads row l%32 of a
 //     32-row block, chunk 2*s + l/32 of sub-step s.  That is one
 //     v_mfma_i32_32x32x32_i8 (16 i8), one v_mfma_f32_32x32x16_bf16 (8 bf16) or
 //     four v_mfma_f32_32x32x2_f32 (1 f32 each) per 32x32 block.  A and B use
 //     the same lane -> k mapping, so each instruction pairs A[i,k] with B[k,j]
 //     whatever order the hardware sums its k values in.
-//   * The next stage's global loads are issued before the current stage's
-//     MFMAs, so their latency hides behind the matrix work.
+//   * The main loop (see mma_kernel) keeps the matrix pipe fed: fragment
+//     reads, the next stages' loads and the stage barrier are interleaved with
+//     the MFMAs, and the next stage's first fragments are read while the
+//     current stage's second half of MFMAs run.
 // The 32x32 accumulator block lives in 16 registers per lane: register r of
 // lane l holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
 #include "epilogue.h"
@@ -73,9 +74,6 @@ struct Mma<InType::F32> {
     }
 };
 
-constexpr int kThreads = 256;
-constexpr int kStageBytes = 128;  // K bytes per row per stage
-
 // Workgroup id -> (tile_m, tile_n).  The hardware hands consecutive workgroup
 // ids to the 8 XCDs round-robin; the first remap gives every XCD one
 // contiguous range of logical ids, and the grouped order below makes each
@@ -97,21 +95,85 @@ __device__ __forceinline__ void tile_coords(int bid, int nblocks, int tiles_m, i
     tn = r / gsize;
 }
 
-template <InType T, EpiKind E, int BM, int BN>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2)))
+// Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
+constexpr int kSchedVmem = 0x010;
+
+// Sixteen zero bytes: the source of the K-tail chunks of a partial last stage
+// (direct-to-LDS loads cannot zero-fill in flight).
+__device__ __attribute__((aligned(16))) uint8_t g_zero_chunk[16];
+
+// A stage holds BK bytes of K for every A and B row of the tile: row r at
+// r*BK, chunk c (16 bytes) in slot c ^ swz(r).  An operand read is 16 lanes
+// per LDS cycle (64 banks of 4 bytes) reading the same chunk of 16 consecutive
+// rows; the swizzle spreads them over 16 distinct 16-byte bank groups.  For
+// BK = 64 (4 chunks per row) rows r and r+4 share bank groups unless their
+// slots differ, hence swz = (r >> 2) & 3; for BK = 128, swz = (r >> 1) & 7.
+template <int BK>
+__device__ __forceinline__ int swz_of(int row) {
+    return BK == 64 ? ((row >> 2) & 3) : ((row >> 1) & 7);
+}
+
+// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt low bits [3:0] and high
+// bits [15:14], expcnt [6:4] left at 7, lgkmcnt [11:8] = 0).  lgkmcnt(0) also
+// retires this wave's LDS reads of the slot the next loads will overwrite.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x70);
+}
+
+// Workgroup barrier for the stage ring.  The caller has already waited for
+// this wave's loads of the stage and for its LDS reads (wait_vmcnt), so every
+// wave passing the barrier means the stage is complete in LDS.  A fence here
+// (even an LDS-only one) would make the compiler drain every direct-to-LDS
+// load in flight, i.e. the later stages too; the memory clobber alone keeps
+// the compiler from moving LDS accesses across the barrier.
+__device__ __forceinline__ void stage_barrier() {
+    asm volatile("s_barrier" ::: "memory");
+}
+
+// Kernel: one workgroup of 4 waves (2 x 2) per BM x BN tile of C.
+//   BK  K bytes per stage (64), NS stages in the LDS ring.
+// Main loop per stage kt:
+//   wait for this wave's loads of stage kt, barrier (every wave's landed);
+//   issue the direct-to-LDS loads of stage kt+NS-1 into the slot stage kt-1
+//   used (every wave finished reading it before the barrier);
+//   MFMAs over stage kt, reading each sub-step's fragments while the previous
+//   sub-step's MFMAs run.
+// Epilogue: each wave stages 32 accumulator rows at a time through LDS and
+// writes them back as row-contiguous 4-element chunks (16-byte stores for
+// i32/f32 output).
+template <int BM, int BN, int WM, int WN>
+constexpr int waves_per_simd() {
+    return (WM * WN > 4 || BM * BN < 256 * 256) ? 2 : 1;
+}
+
+template <InType T, EpiKind E, int BM, int BN, int WM, int WN, int BK, int NS>
+__global__ __launch_bounds__(WM * WN * 64)
+__attribute__((amdgpu_waves_per_eu(waves_per_simd<BM, BN, WM, WN>(),
+                                   waves_per_simd<BM, BN, WM, WN>())))
 void mma_kernel(const MmaArgs args, const EpiParams ep) {
-    constexpr int WM = 2, WN = 2;
+    constexpr int NWAVES = WM * WN;
     constexpr int WTM = BM / WM, WTN = BN / WN;
     constexpr int TM = WTM / 32, TN = WTN / 32;
-    constexpr int A_CH = BM * 8 / kThreads;  // 16-byte chunks per thread per stage
-    constexpr int B_CH = BN * 8 / kThreads;
-    constexpr int A_BYTES = BM * kStageBytes;
-    constexpr int STAGE = (BM + BN) * kStageBytes;
-    static_assert(A_CH >= 1 && B_CH >= 1 && TM >= 1 && TN >= 1, "tile too small");
+    constexpr int STAGE = (BM + BN) * BK;
+    constexpr int A_BYTES = BM * BK;
+    constexpr int NI = STAGE / 1024;      // direct-to-LDS instructions per stage
+    constexpr int NIW = NI / NWAVES;      // ... per wave
+    constexpr int RPI = 1024 / BK;        // stage rows one instruction fills
+    constexpr int CPR = BK / 16;          // 16-byte chunks per stage row
+    constexpr int SUB = BK / 32;          // MFMA sub-steps per stage
+    constexpr int EPI_LD = WTN + 8;       // staged-epilogue row stride (4-byte words)
+    constexpr int SMEM = NS * STAGE;
+    static_assert(NI % NWAVES == 0 && TM >= 1 && TN >= 1, "tile too small");
+    static_assert(NWAVES * 32 * EPI_LD * 4 <= SMEM, "epilogue staging does not fit");
     using M = Mma<T>;
     using acc_t = typename M::acc_t;
+    using val_t = typename M::scalar_t;
 
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -130,55 +192,43 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     const int64_t lda_b = args.lda * esz, ldb_b = args.ldb * esz;
     const uint8_t *A = (const uint8_t *)args.a + z * args.bsa * esz;
     const uint8_t *B = (const uint8_t *)args.b + z * args.bsb * esz;
+    const int KT = (int)((kbytes + BK - 1) / BK);
+    const bool k_whole = (kbytes % BK) == 0;
 
-    // Per-thread global chunk coordinates (fixed across stages).
-    const uint8_t *a_src[A_CH];
-    bool a_ok[A_CH];
-    int a_lds[A_CH];
+    // This lane's source chunk for each of the wave's NIW load instructions:
+    // instruction q fills stage bytes [q*1024, q*1024 + 1024), lane l the 16
+    // bytes at +16*l, i.e. stage row q*RPI + l/CPR, slot l%CPR, which holds
+    // chunk (l%CPR) ^ swz(row).  Rows past the matrix edge read the last row.
+    const uint8_t *src[NIW];
+    int kch[NIW];
 #pragma unroll
-    for (int i = 0; i < A_CH; ++i) {
-        int q = tid + i * kThreads;
-        int row = q >> 3, ch = q & 7;
-        int grow = m0 + row;
-        a_ok[i] = grow < args.M;
-        a_src[i] = A + (int64_t)(a_ok[i] ? grow : 0) * lda_b + ch * 16;
-        a_lds[i] = row * kStageBytes + ((ch ^ (row & 7)) << 4);
-    }
-    const uint8_t *b_src[B_CH];
-    bool b_ok[B_CH];
-    int b_lds[B_CH];
-#pragma unroll
-    for (int i = 0; i < B_CH; ++i) {
-        int q = tid + i * kThreads;
-        int row = q >> 3, ch = q & 7;
-        int gcol = n0 + row;
-        b_ok[i] = gcol < args.N;
-        b_src[i] = B + (int64_t)(b_ok[i] ? gcol : 0) * ldb_b + ch * 16;
-        b_lds[i] = A_BYTES + row * kStageBytes + ((ch ^ (row & 7)) << 4);
-    }
-
-    v4i ra[A_CH], rb[B_CH];
-    auto load_stage = [&](int kt) {
-        const int64_t kb = (int64_t)kt * kStageBytes;
-#pragma unroll
-        for (int i = 0; i < A_CH; ++i) {
-            int ch = (tid + i * kThreads) & 7;
-            bool ok = a_ok[i] && (kb + ch * 16 < kbytes);
-            ra[i] = ok ? *(const v4i *)(a_src[i] + kb) : v4i{0, 0, 0, 0};
+    for (int i = 0; i < NIW; ++i) {
+        const int q = wave * NIW + i;
+        const int row = q * RPI + lane / CPR;
+        const int ch = (lane % CPR) ^ swz_of<BK>(row);
+        kch[i] = ch * 16;
+        if (row < BM) {
+            int g = m0 + row < args.M ? m0 + row : args.M - 1;
+            src[i] = A + (int64_t)g * lda_b + ch * 16;
+        } else {
+            int g = n0 + row - BM < args.N ? n0 + row - BM : args.N - 1;
+            src[i] = B + (int64_t)g * ldb_b + ch * 16;
         }
+    }
+    // Loads of stage kt (clamped to the last stage, see below) into ring slot
+    // `slot`.  The partial last stage reads its chunks past K from zeros.
+    auto issue_stage = [&](int kt, int slot, int first, int count) {
+        kt = kt < KT ? kt : KT - 1;
+        const int64_t kb = (int64_t)kt * BK;
+        uint8_t *dst = smem + slot * STAGE + wave * NIW * 1024;
+        const bool tail = !k_whole && kt == KT - 1;
 #pragma unroll
-        for (int i = 0; i < B_CH; ++i) {
-            int ch = (tid + i * kThreads) & 7;
-            bool ok = b_ok[i] && (kb + ch * 16 < kbytes);
-            rb[i] = ok ? *(const v4i *)(b_src[i] + kb) : v4i{0, 0, 0, 0};
+        for (int i = first; i < first + count; ++i) {
+            const void *g = src[i] + kb;
+            if (tail && kb + kch[i] >= kbytes) g = g_zero_chunk;
+            __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)(dst + i * 1024),
+                                             16, 0, 0);
         }
-    };
-    auto store_stage = [&](int buf) {
-        uint8_t *s = smem + buf * STAGE;
-#pragma unroll
-        for (int i = 0; i < A_CH; ++i) *(v4i *)(s + a_lds[i]) = ra[i];
-#pragma unroll
-        for (int i = 0; i < B_CH; ++i) *(v4i *)(s + b_lds[i]) = rb[i];
     };
 
     acc_t acc[TM][TN];
@@ -187,62 +237,135 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = acc_t{};
 
-    // Operand read offsets within a stage for this lane.
     const int lrow = lane & 31, lhalf = lane >> 5;
     int a_row_off[TM], b_row_off[TN];
 #pragma unroll
-    for (int i = 0; i < TM; ++i) a_row_off[i] = (wm * WTM + i * 32 + lrow) * kStageBytes;
+    for (int i = 0; i < TM; ++i) a_row_off[i] = (wm * WTM + i * 32 + lrow) * BK;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) b_row_off[j] = A_BYTES + (wn * WTN + j * 32 + lrow) * kStageBytes;
-    const int swz = lrow & 7;  // (row & 7) == (lrow & 7): block bases are multiples of 32
+    for (int j = 0; j < TN; ++j) b_row_off[j] = A_BYTES + (wn * WTN + j * 32 + lrow) * BK;
+    const int swz = swz_of<BK>(lrow);  // operand block bases are multiples of 32 rows
 
-    const int KT = (int)((kbytes + kStageBytes - 1) / kStageBytes);
-    load_stage(0);
-    store_stage(0);
-    __syncthreads();
+    v4i af[SUB][TM], bf[SUB][TN];
+    auto read_frags = [&](const uint8_t *s, int ss, int set) {
+        const int slot = ((2 * ss + lhalf) ^ swz) << 4;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) af[set][i] = *(const v4i *)(s + a_row_off[i] + slot);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bf[set][j] = *(const v4i *)(s + b_row_off[j] + slot);
+    };
+    auto mfmas = [&](int set) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] = M::step(af[set][i], bf[set][j], acc[i][j]);
+    };
 
+    // Every iteration issues exactly one stage of loads: past the end of K it
+    // re-reads the last stage into a slot nothing reads again, which keeps the
+    // loop body straight-line code and makes the wait count a constant.  The
+    // full barrier before the epilogue drains these extra loads.
+    //
+    // Lookahead: stage kt+1 is certified complete (wait + barrier) half way
+    // through stage kt, so its first fragments are read under stage kt's
+    // second half of MFMAs and no LDS latency is exposed at a stage boundary.
+    //   phase A: stage kt sub-step 0 MFMAs (fragments F0), with sub-step 1's
+    //            fragment reads (F1) and half of the loads of stage kt+NS-1 --
+    //            into the slot of stage kt-1, finished by every wave before the
+    //            previous barrier -- spread between them;
+    //   barrier: this wave's loads of stage kt+1 landed and its LDS reads
+    //            retired, then s_barrier;
+    //   phase C: sub-step 1 MFMAs (F1), with stage kt+1's sub-step 0 reads
+    //            (into F0) and the other half of the loads spread between them.
+    // Splitting the loads over both phases keeps the CU's address unit (one
+    // 1 KiB load takes it ~16 cycles, and four waves share it) from backing up
+    // into the waves' instruction issue.
+    // The empty asm statements pin F0 and F1 around the barrier so the compiler
+    // keeps each phase's MFMAs on its side.
+    constexpr int H0 = NIW / 2, H1 = NIW - H0;  // loads issued in phase A / C
+#pragma unroll
+    for (int s0 = 0; s0 < NS - 1; ++s0) issue_stage(s0, s0, 0, NIW);
+    wait_vmcnt<(NS - 2) * NIW>();
+    stage_barrier();
+    read_frags(smem, 0, 0);
+
+    static_assert(SUB == 2, "schedule assumes two sub-steps");
     for (int kt = 0; kt < KT; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < KT) load_stage(kt + 1);
-        const uint8_t *s = smem + cur * STAGE;
+        const uint8_t *s = smem + (kt % NS) * STAGE;
+        const int nslot = (kt + NS - 1) % NS;
+        read_frags(s, 1, 1);
+        mfmas(0);
+        issue_stage(kt + NS - 1, nslot, 0, H0);
 #pragma unroll
-        for (int ss = 0; ss < 4; ++ss) {
-            const int slot = ((2 * ss + lhalf) ^ swz) << 4;
-            v4i af[TM], bf[TN];
-#pragma unroll
-            for (int i = 0; i < TM; ++i) af[i] = *(const v4i *)(s + a_row_off[i] + slot);
-#pragma unroll
-            for (int j = 0; j < TN; ++j) bf[j] = *(const v4i *)(s + b_row_off[j] + slot);
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j) acc[i][j] = M::step(af[i], bf[j], acc[i][j]);
+        for (int i = 0; i < TM * TN; ++i) {
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+            if (i < TM + TN) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+            if (i >= TM * TN - H0) __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
         }
-        if (kt + 1 < KT) store_stage(cur ^ 1);
-        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[0][i]));
+#pragma unroll
+        for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bf[0][j]));
+        // Stage kt+1's loads were issued at iteration kt+2-NS; issued after
+        // them: NS-3 whole iterations plus this phase A.
+        wait_vmcnt<(NS - 3) * NIW + H0>();
+        stage_barrier();
+#pragma unroll
+        for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[1][i]));
+#pragma unroll
+        for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bf[1][j]));
+        read_frags(smem + ((kt + 1) % NS) * STAGE, 0, 0);
+        mfmas(1);
+        issue_stage(kt + NS - 1, nslot, H0, H1);
+#pragma unroll
+        for (int i = 0; i < TM * TN; ++i) {
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+            if (i < TM + TN) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+            if (i >= TM * TN - H1) __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
+        }
     }
 
-    // Epilogue on the accumulator registers.
+    // Staged epilogue.  Wave region: 32 rows x EPI_LD words.  Written from the
+    // MFMA layout (register r of lane l: row 8*(r/4) + 4*(l/32) + r%4, column
+    // l%32 of block j), read back as 4-column chunks, one row per CPRE lanes.
+    __syncthreads();
+    val_t *stg = (val_t *)smem + wave * 32 * EPI_LD;
+    constexpr int CPRE = WTN / 4;          // 4-column chunks per staged row
+    constexpr int RPIT = 64 / CPRE;        // rows per read iteration
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int col = n0 + wn * WTN + j * 32 + lrow;
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm * WTM + i * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
-                if (row < args.M && col < args.N)
-                    Store<E>::apply(ep, z, row, col, acc[i][j][r]);
+                const int row = (r >> 2) * 8 + lhalf * 4 + (r & 3);
+                stg[row * EPI_LD + j * 32 + lrow] = (val_t)acc[i][j][r];
             }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes done
+        __builtin_amdgcn_wave_barrier();
+        const int grow0 = m0 + wm * WTM + i * 32;
+        const int gcol0 = n0 + wn * WTN;
+#pragma unroll
+        for (int it = 0; it < 32 / RPIT; ++it) {
+            const int row = it * RPIT + lane / CPRE;
+            const int c4 = (lane % CPRE) * 4;
+            typedef val_t v4_t __attribute__((ext_vector_type(4)));
+            v4_t v4 = *(const v4_t *)(stg + row * EPI_LD + c4);
+            val_t v[4] = {v4[0], v4[1], v4[2], v4[3]};
+            const int grow = grow0 + row;
+            if (grow < args.M && gcol0 + c4 < args.N)
+                store4<E, val_t>(ep, z, grow, gcol0 + c4, args.N, v);
         }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_wave_barrier();
     }
 }
 
-template <InType T, EpiKind E, int BM, int BN>
+template <InType T, EpiKind E, int BM, int BN, int WM, int WN, int NS = 4>
 static hipError_t launch_one(const MmaArgs &args, const EpiParams &ep, hipStream_t stream) {
     int tiles = ((args.M + BM - 1) / BM) * ((args.N + BN - 1) / BN);
     dim3 grid(tiles, 1, args.batch);
-    hipLaunchKernelGGL((mma_kernel<T, E, BM, BN>), grid, dim3(kThreads), 0, stream, args, ep);
+    hipLaunchKernelGGL((mma_kernel<T, E, BM, BN, WM, WN, 64, NS>), grid, dim3(WM * WN * 64), 0,
+                       stream, args, ep);
     return hipGetLastError();
 }
 
@@ -250,10 +373,12 @@ template <InType T, EpiKind E>
 static hipError_t launch_tile(Tile tile, const MmaArgs &args, const EpiParams &ep,
                               hipStream_t stream) {
     switch (tile) {
-    case Tile::T256x256: return launch_one<T, E, 256, 256>(args, ep, stream);
-    case Tile::T256x128: return launch_one<T, E, 256, 128>(args, ep, stream);
-    case Tile::T128x128: return launch_one<T, E, 128, 128>(args, ep, stream);
-    case Tile::T64x64: return launch_one<T, E, 64, 64>(args, ep, stream);
+    case Tile::T256x256: return launch_one<T, E, 256, 256, 2, 2>(args, ep, stream);
+    case Tile::T256x256w8: return launch_one<T, E, 256, 256, 2, 4>(args, ep, stream);
+    case Tile::T256x128: return launch_one<T, E, 256, 128, 2, 2>(args, ep, stream);
+    case Tile::T256x128o2: return launch_one<T, E, 256, 128, 2, 2, 3>(args, ep, stream);
+    case Tile::T128x128: return launch_one<T, E, 128, 128, 2, 2>(args, ep, stream);
+    case Tile::T64x64: return launch_one<T, E, 64, 64, 2, 2>(args, ep, stream);
     }
     return hipErrorInvalidValue;
 }
