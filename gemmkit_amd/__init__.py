@@ -53,6 +53,7 @@ __all__ = [
     "gemm_i8_unchecked", "gemm_i8_requant", "gemm_i8_requant_u8", "gemm_i8_requant_unchecked",
     "gemm_i8_requant_u8_unchecked", "prepack_rhs_i8", "gemm_i8_packed_b",
     "gemm_i8_packed_b_unchecked", "gemm_i8_packed_b_requant", "gemm_i8_packed_b_requant_u8",
+    "gemm_i8_packed_b_requant_unchecked",
     "gemm_batched", "gemm_batched_unchecked", "gemm_batched_bf16_f32out", "set_synchronous",
     "library_path", "version",
 ]
@@ -431,6 +432,19 @@ def gemm_i8_packed_b_requant_u8(a: MatRef, packed: PackedRhs, req: Requantize, c
     _check(_lib.lib().gk_gemm_i8_packed_b_requant_u8(_ws(ws), a._c(torch.int8, "A"),
                                                      packed.handle, C.byref(req._c()),
                                                      c._c(torch.uint8, "C"), _par(par)))
+
+
+def gemm_i8_packed_b_requant_unchecked(m, a, rsa, csa, packed: PackedRhs, scale, scales,
+                                       zero_point, bias, c, rsc, csc, par=None, ws=None,
+                                       axis=0, relu=False, u8=False, a_off=0, c_off=0) -> None:
+    """Extension: unchecked prepacked-B requant (no validation, no host copies)."""
+    _bind_stream()
+    fn = (_lib.lib().gk_gemm_i8_packed_b_requant_u8_unchecked if u8
+          else _lib.lib().gk_gemm_i8_packed_b_requant_unchecked)
+    _check(fn(_ws(ws), m, _ptr(a, a_off), rsa, csa, packed.handle, float(scale), _ptr(scales),
+              1 if scales is not None else 0, int(zero_point), _ptr(bias),
+              1 if bias is not None else 0, _ptr(c, c_off), rsc, csc, _par(par), int(axis),
+              1 if relu else 0))
 
 
 # ------------------------------------------------------------------- batched

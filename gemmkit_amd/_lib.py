@@ -86,6 +86,12 @@ SIGNATURES: dict[str, tuple] = {
                                                 _i32, _vp, _sdiff, _sdiff, _u32]),
     "gk_gemm_i8_packed_b_requant": (C.c_int, [_vp, _REF, _vp, _REQ, _MUT, _u32]),
     "gk_gemm_i8_packed_b_requant_u8": (C.c_int, [_vp, _REF, _vp, _REQ, _MUT, _u32]),
+    "gk_gemm_i8_packed_b_requant_unchecked": (C.c_int, [_vp, _size, _vp, _sdiff, _sdiff, _vp, _f32,
+                                                        _vp, _u8, _i32, _vp, _u8, _vp, _sdiff,
+                                                        _sdiff, _u32, _i32, _i32]),
+    "gk_gemm_i8_packed_b_requant_u8_unchecked": (C.c_int, [_vp, _size, _vp, _sdiff, _sdiff, _vp,
+                                                           _f32, _vp, _u8, _i32, _vp, _u8, _vp,
+                                                           _sdiff, _sdiff, _u32, _i32, _i32]),
     "gk_gemm_batched_f32": (C.c_int, [_vp, _size, _f32, _REF, _sdiff, _REF, _sdiff, _f32, _MUT,
                                       _sdiff, _u32]),
     "gk_gemm_batched_f32_unchecked": (C.c_int, [_vp, _size, _size, _size, _size, _f32, _vp,

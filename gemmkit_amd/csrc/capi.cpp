@@ -952,6 +952,32 @@ int gk_gemm_i8_packed_b_requant_u8(gk_workspace *ws, const gk_mat_ref *a,
     return requant_checked(ws, a, nullptr, packed, req, c, true);
 }
 
+int gk_gemm_i8_packed_b_requant_unchecked(gk_workspace *ws, size_t m, const int8_t *a,
+                                          ptrdiff_t rsa, ptrdiff_t csa,
+                                          const gk_packed_rhs *packed, float scale,
+                                          const float *scales, uint8_t has_scales,
+                                          int32_t zero_point, const int32_t *bias,
+                                          uint8_t has_bias, int8_t *c, ptrdiff_t rsc,
+                                          ptrdiff_t csc, gk_par, int32_t axis, int32_t act) {
+    if (!packed) return fail(GK_ERR_ARG, "gemmkit: null packed RHS");
+    return exec_requant(ws, m, packed->k, packed->n, a, rsa, csa, nullptr, 0, 0, scale,
+                        has_scales ? scales : nullptr, zero_point, has_bias ? bias : nullptr, axis,
+                        act, -128, 127, c, rsc, csc, packed);
+}
+
+int gk_gemm_i8_packed_b_requant_u8_unchecked(gk_workspace *ws, size_t m, const int8_t *a,
+                                             ptrdiff_t rsa, ptrdiff_t csa,
+                                             const gk_packed_rhs *packed, float scale,
+                                             const float *scales, uint8_t has_scales,
+                                             int32_t zero_point, const int32_t *bias,
+                                             uint8_t has_bias, uint8_t *c, ptrdiff_t rsc,
+                                             ptrdiff_t csc, gk_par, int32_t axis, int32_t act) {
+    if (!packed) return fail(GK_ERR_ARG, "gemmkit: null packed RHS");
+    return exec_requant(ws, m, packed->k, packed->n, a, rsa, csa, nullptr, 0, 0, scale,
+                        has_scales ? scales : nullptr, zero_point, has_bias ? bias : nullptr, axis,
+                        act, 0, 255, c, rsc, csc, packed);
+}
+
 // ---- batched (src/api/batched.rs:188-711)
 
 int gk_gemm_batched_f32_unchecked(gk_workspace *ws, size_t batch, size_t m, size_t k, size_t n,

@@ -249,6 +249,23 @@ int gk_gemm_i8_packed_b_requant(gk_workspace *ws, const gk_mat_ref *a,
 int gk_gemm_i8_packed_b_requant_u8(gk_workspace *ws, const gk_mat_ref *a,
                                    const gk_packed_rhs *packed, const gk_requantize *req,
                                    const gk_mat_mut *c, gk_par par);
+/* Unchecked twins of the two entries above (raw A/C pointers and strides, the
+ * requant fields as gk_gemm_i8_requant_unchecked takes them); no validation. */
+int gk_gemm_i8_packed_b_requant_unchecked(gk_workspace *ws, size_t m, const int8_t *a,
+                                          ptrdiff_t rsa, ptrdiff_t csa,
+                                          const gk_packed_rhs *packed, float scale,
+                                          const float *scales, uint8_t has_scales,
+                                          int32_t zero_point, const int32_t *bias,
+                                          uint8_t has_bias, int8_t *c, ptrdiff_t rsc,
+                                          ptrdiff_t csc, gk_par par, int32_t axis, int32_t act);
+int gk_gemm_i8_packed_b_requant_u8_unchecked(gk_workspace *ws, size_t m, const int8_t *a,
+                                             ptrdiff_t rsa, ptrdiff_t csa,
+                                             const gk_packed_rhs *packed, float scale,
+                                             const float *scales, uint8_t has_scales,
+                                             int32_t zero_point, const int32_t *bias,
+                                             uint8_t has_bias, uint8_t *c, ptrdiff_t rsc,
+                                             ptrdiff_t csc, gk_par par, int32_t axis,
+                                             int32_t act);
 
 /* ----------------------------------------------------------- batched GEMM */
 
