@@ -430,6 +430,12 @@ int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t
         ep.vec4 = ep.csc == 1 && (M == 1 || ep.rsc % 4 == 0) && (batch <= 1 || bsc % 4 == 0) &&
                   ((uintptr_t)c % (uintptr_t)(4 * osz)) == 0;
     }
+    // The matrix-core kernels address a tile's rows with 32-bit offsets from
+    // the tile's first row: 256 rows of either operand must span < 2 GiB.
+    if (std::max(A.rs, Bt.rs) * (int64_t)esz > kMaxTileRowBytes)
+        return fail(GK_ERR_OVERFLOW,
+                    "gemmkit: row stride too large for the device kernels (more than %lld "
+                    "elements per row)", (long long)(kMaxTileRowBytes / (int64_t)esz));
     MmaArgs args{};
     args.a = A.p;
     args.b = Bt.p;

@@ -39,6 +39,10 @@ struct EpiParams {
     int32_t vec4;          // C is unit-stride along columns and 4-element aligned
 };
 
+// Largest operand row stride (bytes) the matrix-core kernels address: 256 rows
+// of a tile stay below 2^31 bytes of 32-bit buffer offsets.
+constexpr int64_t kMaxTileRowBytes = 0x7FFFFFF0 / 256;
+
 struct MmaArgs {
     const void *a;         // M x K, k-contiguous
     const void *b;         // N x K, k-contiguous

@@ -7,9 +7,12 @@
 //
 // Data path (one workgroup = 4 or 8 waves of 64 lanes over one tile):
 //   * K advances in stages of 64 bytes per row (64 i8, 32 bf16, 16 f32).  The
-//     stage's A and B rows go global -> LDS with direct-to-LDS loads
-//     (global_load_lds_dwordx4: lane l of an instruction fills LDS bytes
+//     stage's A and B rows go global -> LDS with direct-to-LDS buffer loads
+//     (buffer_load_dwordx4 ... lds: lane l of an instruction fills LDS bytes
 //     base + 16*l), into a ring of NS stages, so no VGPRs stage the operands.
+//     A 32-bit offset per lane (not a 64-bit address) halves the address
+//     traffic of each load, and the resource's range check supplies the zero
+//     padding of edge tiles and of the K tail.
 //     Row r of a stage stores its chunk c (16 bytes) in slot c ^ swz(r), which
 //     keeps the operand reads below free of LDS bank conflicts.
 //   * Every MFMA operand is 16 bytes per lane: lane l reads row l%32 of a
@@ -100,9 +103,25 @@ constexpr int kSchedMfma = 0x008;
 constexpr int kSchedDsRead = 0x100;
 constexpr int kSchedVmem = 0x010;
 
-// Sixteen zero bytes: the source of the K-tail chunks of a partial last stage
-// (direct-to-LDS loads cannot zero-fill in flight).
-__device__ __attribute__((aligned(16))) uint8_t g_zero_chunk[16];
+// Operand loads go through buffer resources (base + 32-bit per-lane offset,
+// range-checked by the address unit): a lane whose offset is at or past the
+// resource's size reads zeros and touches no memory.  That zero-fills the rows
+// past the matrix edge and the K tail of the last stage, and lets the loop
+// issue its loads past the end of K without traffic.  Offsets stay below
+// kMaxRecords, which the host guarantees for every in-range byte of a tile.
+constexpr uint32_t kMaxRecords = 0x7FFFFFF0u;
+constexpr uint32_t kOutOfRange = 0x80000000u;
+constexpr int kRsrcWord3 = 0x00020000;  // raw (unswizzled) buffer, 32-bit data format
+
+// One direct-to-LDS load of 16 bytes per lane: lane l reads base[voff] into
+// LDS bytes lds + 16*l (zeros when voff >= num).
+__device__ __forceinline__ void dma16(const uint8_t *base, uint32_t num, uint32_t voff,
+                                      uint8_t *lds) {
+    __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)num, kRsrcWord3);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16,
+                                             voff, 0, 0, 0);
+}
 
 // A stage holds BK bytes of K for every A and B row of the tile: row r at
 // r*BK, chunk c (16 bytes) in slot c ^ swz(r).  An operand read is 16 lanes
@@ -177,7 +196,7 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps load setup scalar
     const int wm = wave / WN, wn = wave % WN;
 
     const int tiles_m = (args.M + BM - 1) / BM;
@@ -195,39 +214,44 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     const int KT = (int)((kbytes + BK - 1) / BK);
     const bool k_whole = (kbytes % BK) == 0;
 
+    // The tile's A rows [m0, m0+BM) and B rows [n0, n0+BN) as two buffer
+    // resources; rows past the matrix edge fall outside them and read zeros.
+    const uint8_t *a_pan = A + (int64_t)m0 * lda_b;
+    const uint8_t *b_pan = B + (int64_t)n0 * ldb_b;
+    const uint32_t a_num = (uint32_t)((args.M - m0 < BM ? args.M - m0 : BM) * lda_b);
+    const uint32_t b_num = (uint32_t)((args.N - n0 < BN ? args.N - n0 : BN) * ldb_b);
+
     // This lane's source chunk for each of the wave's NIW load instructions:
     // instruction q fills stage bytes [q*1024, q*1024 + 1024), lane l the 16
     // bytes at +16*l, i.e. stage row q*RPI + l/CPR, slot l%CPR, which holds
-    // chunk (l%CPR) ^ swz(row).  Rows past the matrix edge read the last row.
-    const uint8_t *src[NIW];
+    // chunk (l%CPR) ^ swz(row).  Each instruction covers RPI whole rows, all
+    // of A or all of B (BM is a multiple of RPI), so from_a is wave-uniform.
+    uint32_t voff[NIW];
     int kch[NIW];
+    bool from_a[NIW];
 #pragma unroll
     for (int i = 0; i < NIW; ++i) {
         const int q = wave * NIW + i;
         const int row = q * RPI + lane / CPR;
         const int ch = (lane % CPR) ^ swz_of<BK>(row);
         kch[i] = ch * 16;
-        if (row < BM) {
-            int g = m0 + row < args.M ? m0 + row : args.M - 1;
-            src[i] = A + (int64_t)g * lda_b + ch * 16;
-        } else {
-            int g = n0 + row - BM < args.N ? n0 + row - BM : args.N - 1;
-            src[i] = B + (int64_t)g * ldb_b + ch * 16;
-        }
+        from_a[i] = q * RPI < BM;
+        voff[i] = from_a[i] ? (uint32_t)(row * lda_b + ch * 16)
+                            : (uint32_t)((row - BM) * ldb_b + ch * 16);
     }
-    // Loads of stage kt (clamped to the last stage, see below) into ring slot
-    // `slot`.  The partial last stage reads its chunks past K from zeros.
+    // Loads of stage kt into ring slot `slot`.  Stages past the end of K load
+    // nothing but zeros (every lane out of range), as do the chunks past K of
+    // a partial last stage.
     auto issue_stage = [&](int kt, int slot, int first, int count) {
-        kt = kt < KT ? kt : KT - 1;
-        const int64_t kb = (int64_t)kt * BK;
+        const uint32_t kb = (uint32_t)kt * BK;
         uint8_t *dst = smem + slot * STAGE + wave * NIW * 1024;
+        const bool dead = kt >= KT;
         const bool tail = !k_whole && kt == KT - 1;
 #pragma unroll
         for (int i = first; i < first + count; ++i) {
-            const void *g = src[i] + kb;
-            if (tail && kb + kch[i] >= kbytes) g = g_zero_chunk;
-            __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)(dst + i * 1024),
-                                             16, 0, 0);
+            uint32_t off = voff[i] + kb;
+            if (dead || (tail && (int64_t)kb + kch[i] >= kbytes)) off = kOutOfRange;
+            dma16(from_a[i] ? a_pan : b_pan, from_a[i] ? a_num : b_num, off, dst + i * 1024);
         }
     };
 
@@ -260,10 +284,10 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
             for (int j = 0; j < TN; ++j) acc[i][j] = M::step(af[set][i], bf[set][j], acc[i][j]);
     };
 
-    // Every iteration issues exactly one stage of loads: past the end of K it
-    // re-reads the last stage into a slot nothing reads again, which keeps the
-    // loop body straight-line code and makes the wait count a constant.  The
-    // full barrier before the epilogue drains these extra loads.
+    // Every iteration issues exactly one stage of loads: past the end of K they
+    // are out-of-range loads (zeros into a slot nothing reads again, no memory
+    // traffic), which keeps the loop body straight-line code and makes the
+    // wait count a constant.  The full barrier before the epilogue drains them.
     //
     // Lookahead: stage kt+1 is certified complete (wait + barrier) half way
     // through stage kt, so its first fragments are read under stage kt's
