@@ -324,6 +324,13 @@ Tile env_tile(bool *forced) {
     return Tile::T256x256;
 }
 
+// GEMMKIT_HIP_SKINNY=0 keeps products with a short side of 1..8 on the
+// wavefront-reduction GEMV instead of the matrix-core skinny kernel.
+bool skinny_enabled() {
+    const char *s = getenv("GEMMKIT_HIP_SKINNY");
+    return !(s && !strcmp(s, "0"));
+}
+
 // Tile table: per shape, the tile that minimises waves x per-wave work, where
 // a CU holds `occ` workgroups of a tile at once and `eff` is the tile's
 // relative matrix-core efficiency.
@@ -397,11 +404,21 @@ int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t
     }
 
     hipError_t e;
-    if ((M <= 8 || N <= 8) && std::max(M, N) >= 1) {
-        // GEMV route: the short side's rows are the vectors.
+    const int64_t short_side = std::min(M, N);
+    // The matrix-core kernels address a tile's rows with 32-bit offsets from
+    // its first row: 256 row strides plus a row must stay below 2 GiB.
+    const bool offsets_fit = std::max(A.rs, Bt.rs) * (int64_t)esz <= kMaxTileRowBytes &&
+                             k * (int64_t)esz <= kMaxTileRowBytes;
+    const bool skinny_ok = short_side <= 16 && skinny_enabled() && offsets_fit &&
+                           skinny_lds_bytes(in, k, (int)short_side) <= kSkinnyLdsMax;
+    if (skinny_ok || short_side <= 8) {
+        // Skinny route: the short side's rows are the vectors, streamed
+        // against the long side's rows (matrix-core kernel up to 16 vectors
+        // when the vectors fit in LDS, else the wavefront-reduction GEMV).
+        const bool vec_is_a = M <= N;
         GemvArgs g{};
         EpiParams eg = ep;
-        if (M <= 8) {
+        if (vec_is_a) {
             g.mat = Bt.p; g.ld = Bt.rs; g.vec = A.p; g.vld = A.rs; g.R = (int32_t)N; g.nvec = (int32_t)M;
         } else {
             g.mat = A.p; g.ld = A.rs; g.vec = Bt.p; g.vld = Bt.rs; g.R = (int32_t)M; g.nvec = (int32_t)N;
@@ -409,18 +426,20 @@ int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t
             eg.axis ^= 1;
         }
         g.K = (int32_t)k;
-        const Opnd &mat = (M <= 8) ? Bt : A;
-        const Opnd &vec = (M <= 8) ? A : Bt;
+        g.cus = g_num_cus;
+        const Opnd &mat = vec_is_a ? Bt : A;
+        const Opnd &vec = vec_is_a ? A : Bt;
+        const int64_t osz = ep.kind == EpiKind::Q8 ? 1 : (ep.kind == EpiKind::BF16 ? 2 : 4);
         for (int64_t z = 0; z < batch; ++z) {
             GemvArgs gz = g;
             gz.mat = (const uint8_t *)mat.p + z * mat.bs * (int64_t)esz;
             gz.vec = (const uint8_t *)vec.p + z * vec.bs * (int64_t)esz;
             EpiParams ez = eg;
-            ez.c = (uint8_t *)ep.c + z * bsc * (int64_t)(ep.kind == EpiKind::Q8 ? 1 : (ep.kind == EpiKind::BF16 ? 2 : 4));
-            e = launch_gemv(in, gz, ez, tl_stream);
-            if (e != hipSuccess) return hip_fail(e, "gemv launch");
+            ez.c = (uint8_t *)ep.c + z * bsc * osz;
+            e = skinny_ok ? launch_skinny(in, gz, ez, tl_stream) : launch_gemv(in, gz, ez, tl_stream);
+            if (e != hipSuccess) return hip_fail(e, skinny_ok ? "skinny launch" : "gemv launch");
         }
-        return finish("gemv");
+        return finish(skinny_ok ? "skinny" : "gemv");
     }
 
     // Whole 4-element output chunks can go out as one vector access when C is
@@ -430,12 +449,10 @@ int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t
         ep.vec4 = ep.csc == 1 && (M == 1 || ep.rsc % 4 == 0) && (batch <= 1 || bsc % 4 == 0) &&
                   ((uintptr_t)c % (uintptr_t)(4 * osz)) == 0;
     }
-    // The matrix-core kernels address a tile's rows with 32-bit offsets from
-    // the tile's first row: 256 rows of either operand must span < 2 GiB.
-    if (std::max(A.rs, Bt.rs) * (int64_t)esz > kMaxTileRowBytes)
+    if (!offsets_fit)
         return fail(GK_ERR_OVERFLOW,
-                    "gemmkit: row stride too large for the device kernels (more than %lld "
-                    "elements per row)", (long long)(kMaxTileRowBytes / (int64_t)esz));
+                    "gemmkit: rows too long for the device kernels (K or a row stride above "
+                    "%lld elements)", (long long)(kMaxTileRowBytes / (int64_t)esz));
     MmaArgs args{};
     args.a = A.p;
     args.b = Bt.p;

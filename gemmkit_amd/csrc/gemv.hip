@@ -6,10 +6,23 @@
 // not depend on the route because wrapping i32 addition is associative).
 //
 // out[j, r] = epi( sum_p mat[r, p] * vec[j, p] ),  r < R rows, j < nvec <= 8.
-// The matrix streams from HBM exactly once with 16-byte loads; the nvec
-// vectors are staged once per workgroup in LDS.  Each wave owns RPW rows at a
-// time and keeps RPW x UNROLL loads in flight per lane; partial sums are
-// reduced across the wave with cross-lane shuffles.
+//
+// The matrix streams from HBM exactly once, as 16-byte nontemporal loads; it is
+// the only large operand, so the kernels are built around keeping enough of it
+// in flight.  A row is split into 16-byte chunks; lane l of a wave owns chunks
+// l, l+64, l+128, ... of every row it visits, so the vector chunks a lane
+// multiplies are the same for every row.  Waves are persistent (a grid of a
+// few workgroups per CU) and walk row groups with a grid stride:
+//   * gemv_reg: rows of at most 64*CPL chunks.  Each lane loads its vector
+//     chunks once into registers; the next row group's matrix loads are issued
+//     before the current group is multiplied, so one group is always in flight
+//     behind the arithmetic.
+//   * gemv_lds: longer rows.  The vectors are staged once per workgroup in LDS
+//     and each lane keeps UNROLL chunks per row in flight.
+// Per-lane partial sums of the RPW x NV outputs of a row group are combined by
+// a butterfly over the 64 lanes that halves the number of values each lane
+// carries at every step (V values cost V-1 + log2(64/V) shuffles instead of
+// 6*V), leaving output v on lanes [v*64/V, (v+1)*64/V).
 #include "epilogue.h"
 
 namespace gk {
@@ -30,10 +43,6 @@ struct Dot16<InType::I8> {
         acc = __builtin_amdgcn_sdot4(m[3], x[3], acc, false);
         return acc;
     }
-    __device__ __forceinline__ static acc_t reduce(acc_t v) {
-        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-        return v;
-    }
 };
 
 template <>
@@ -46,10 +55,6 @@ struct Dot16<InType::F32> {
         acc = __builtin_fmaf(a[2], b[2], acc);
         acc = __builtin_fmaf(a[3], b[3], acc);
         return acc;
-    }
-    __device__ __forceinline__ static acc_t reduce(acc_t v) {
-        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-        return v;
     }
 };
 
@@ -65,134 +70,269 @@ struct Dot16<InType::BF16> {
         }
         return acc;
     }
-    __device__ __forceinline__ static acc_t reduce(acc_t v) {
-        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-        return v;
-    }
 };
+
+// Butterfly over the wave: on entry v[0..V) are this lane's partial sums of V
+// outputs; on exit v[0] holds the wave total of output (lane >> (6 - log2 V)).
+template <int V, typename A>
+__device__ __forceinline__ void wave_reduce(A (&v)[V]) {
+    static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "V must be a power of two <= 64");
+    const int lane = threadIdx.x & 63;
+    int n = V;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        if (n > 1) {
+            const bool hi = (lane & off) != 0;
+            const int h = n / 2;
+#pragma unroll
+            for (int i = 0; i < V / 2; ++i) {
+                if (i < h) {
+                    A send = hi ? v[i] : v[i + h];
+                    A keep = hi ? v[i + h] : v[i];
+                    v[i] = keep + __shfl_xor(send, off, 64);
+                }
+            }
+            n = h;
+        } else {
+            v[0] += __shfl_xor(v[0], off, 64);
+        }
+    }
+}
 
 constexpr int kGemvThreads = 256;
 constexpr int kGemvWaves = kGemvThreads / 64;
-constexpr int kUnroll = 4;
+
+template <int V>
+constexpr int log2c() {
+    return V <= 1 ? 0 : 1 + log2c<V / 2>();
+}
+
+// Stores the reduced outputs of row group [r0, r0 + RPW): output index
+// v = r*NV + j lives on lanes [v*64/V, ...); its first lane stores it.
+template <InType T, EpiKind E, int NV, int RPW, typename A>
+__device__ __forceinline__ void store_group(const GemvArgs &g, const EpiParams &ep, int64_t r0,
+                                            const A (&v)[RPW * NV]) {
+    constexpr int V = RPW * NV;
+    constexpr int SH = 6 - log2c<V>();
+    const int lane = threadIdx.x & 63;
+    if ((lane & ((1 << SH) - 1)) == 0) {
+        const int idx = lane >> SH;
+        const int r = idx / NV, j = idx % NV;
+        if (j < g.nvec && r0 + r < g.R) Store<E>::apply(ep, 0, j, (int)(r0 + r), v[0]);
+    }
+}
+
+template <InType T, EpiKind E, int NV, int CPL, int RPW>
+__global__ __launch_bounds__(kGemvThreads) void gemv_reg(const GemvArgs g, const EpiParams ep) {
+    using D = Dot16<T>;
+    using acc_t = typename D::acc_t;
+    constexpr int esz = (T == InType::I8) ? 1 : (T == InType::BF16 ? 2 : 4);
+    // A K*esz that is not a multiple of 16 only reaches this kernel through
+    // the pack, which zero-fills both operands' rows up to the next 16 bytes.
+    const int nch = (int)(((int64_t)g.K * esz + 15) / 16);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint8_t *mat = (const uint8_t *)g.mat;
+    const uint8_t *vec = (const uint8_t *)g.vec;
+    const int64_t ld_b = g.ld * esz, vld_b = g.vld * esz;
+
+    v4i_g x[NV][CPL];
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int u = 0; u < CPL; ++u) {
+            const int c = lane + 64 * u;
+            x[j][u] = (j < g.nvec && c < nch) ? *(const v4i_g *)(vec + j * vld_b + (int64_t)c * 16)
+                                              : v4i_g{0, 0, 0, 0};
+        }
+
+    const int64_t groups = ((int64_t)g.R + RPW - 1) / RPW;
+    const int64_t stride = (int64_t)gridDim.x * kGemvWaves;
+    auto load = [&](int64_t grp, v4i_g (&m)[RPW][CPL]) {
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            int64_t row = grp * RPW + r;
+            row = row < g.R ? row : g.R - 1;
+            const uint8_t *p = mat + row * ld_b;
+#pragma unroll
+            for (int u = 0; u < CPL; ++u) {
+                const int c = lane + 64 * u;
+                m[r][u] = c < nch ? __builtin_nontemporal_load((const v4i_g *)(p + (int64_t)c * 16))
+                                  : v4i_g{0, 0, 0, 0};
+            }
+        }
+    };
+
+    int64_t grp = (int64_t)blockIdx.x * kGemvWaves + wave;
+    if (grp >= groups) return;
+    v4i_g cur[RPW][CPL], nxt[RPW][CPL];
+    load(grp, nxt);
+    for (; grp < groups; grp += stride) {
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+#pragma unroll
+            for (int u = 0; u < CPL; ++u) cur[r][u] = nxt[r][u];
+        if (grp + stride < groups) load(grp + stride, nxt);
+        acc_t v[RPW * NV];
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                acc_t a = acc_t(0);
+#pragma unroll
+                for (int u = 0; u < CPL; ++u) a = D::dot(cur[r][u], x[j][u], a);
+                v[r * NV + j] = a;
+            }
+        wave_reduce(v);
+        store_group<T, E, NV, RPW>(g, ep, grp * RPW, v);
+    }
+}
 
 // Largest staged vector block (bytes) a workgroup keeps in LDS.
 constexpr int kGemvLdsMax = 64 * 1024;
+constexpr int kLdsUnroll = 8;
 
 template <InType T, EpiKind E, int NV, int RPW>
-__global__ __launch_bounds__(kGemvThreads) void gemv_kernel(const GemvArgs g, const EpiParams ep) {
+__global__ __launch_bounds__(kGemvThreads) void gemv_lds(const GemvArgs g, const EpiParams ep) {
     using D = Dot16<T>;
     using acc_t = typename D::acc_t;
     extern __shared__ __attribute__((aligned(16))) uint8_t sv[];
-    const int esz = (T == InType::I8) ? 1 : (T == InType::BF16 ? 2 : 4);
-    // 16-byte chunks per row.  A K*esz that is not a multiple of 16 only reaches
-    // this kernel through the pack, which zero-fills both operands' rows up to
-    // the next 16 bytes, so the padded tail adds nothing.
+    constexpr int esz = (T == InType::I8) ? 1 : (T == InType::BF16 ? 2 : 4);
     const int64_t nch = ((int64_t)g.K * esz + 15) / 16;
-    const int nvec = g.nvec;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint8_t *vec = (const uint8_t *)g.vec;
     const int64_t vld_b = g.vld * esz;
-    const bool staged = (int64_t)nvec * nch * 16 <= kGemvLdsMax;
+    // Vectors beyond nvec (up to NV) read as zeros; when the block does not
+    // fit in LDS the vectors are read from global memory (L2-resident).
+    const bool staged = (int64_t)NV * nch * 16 <= kGemvLdsMax;
     if (staged) {
-        for (int64_t c = tid; c < nvec * nch; c += kGemvThreads) {
-            int64_t j = c / nch, ch = c % nch;
-            *(v4i_g *)(sv + c * 16) = *(const v4i_g *)(vec + j * vld_b + ch * 16);
+        for (int64_t c = tid; c < NV * nch; c += kGemvThreads) {
+            const int64_t j = c / nch, ch = c % nch;
+            *(v4i_g *)(sv + c * 16) = j < g.nvec ? *(const v4i_g *)(vec + j * vld_b + ch * 16)
+                                                 : v4i_g{0, 0, 0, 0};
         }
         __syncthreads();
     }
+    auto xchunk = [&](int j, int64_t ch) -> v4i_g {
+        if (staged) return *(const v4i_g *)(sv + (j * nch + ch) * 16);
+        return j < g.nvec ? *(const v4i_g *)(vec + j * vld_b + ch * 16) : v4i_g{0, 0, 0, 0};
+    };
     const uint8_t *mat = (const uint8_t *)g.mat;
     const int64_t ld_b = g.ld * esz;
-    const int64_t total_waves = (int64_t)gridDim.x * kGemvWaves;
-    for (int64_t r0 = ((int64_t)blockIdx.x * kGemvWaves + wave) * RPW; r0 < g.R;
-         r0 += total_waves * RPW) {
+    const int64_t groups = ((int64_t)g.R + RPW - 1) / RPW;
+    const int64_t stride = (int64_t)gridDim.x * kGemvWaves;
+    for (int64_t grp = (int64_t)blockIdx.x * kGemvWaves + wave; grp < groups; grp += stride) {
+        const int64_t r0 = grp * RPW;
+        const uint8_t *rowp[RPW];
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) rowp[r] = mat + (r0 + r < g.R ? r0 + r : g.R - 1) * ld_b;
         acc_t acc[RPW][NV];
 #pragma unroll
         for (int r = 0; r < RPW; ++r)
 #pragma unroll
             for (int j = 0; j < NV; ++j) acc[r][j] = acc_t(0);
-        const uint8_t *rowp[RPW];
-        bool rok[RPW];
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-            rok[r] = r0 + r < g.R;
-            rowp[r] = mat + (rok[r] ? r0 + r : r0) * ld_b;
-        }
         int64_t ch = lane;
-        for (; ch + 64 * (kUnroll - 1) < nch; ch += 64 * kUnroll) {
-            v4i_g m[kUnroll][RPW];
+        for (; ch + 64 * (kLdsUnroll - 1) < nch; ch += 64 * kLdsUnroll) {
+            v4i_g m[kLdsUnroll][RPW];
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u)
+            for (int u = 0; u < kLdsUnroll; ++u)
 #pragma unroll
                 for (int r = 0; r < RPW; ++r)
                     m[u][r] = __builtin_nontemporal_load((const v4i_g *)(rowp[r] + (ch + 64 * u) * 16));
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
+            for (int u = 0; u < kLdsUnroll; ++u)
 #pragma unroll
                 for (int j = 0; j < NV; ++j) {
-                    if (j < nvec) {
-                        const int64_t xc = j * nch + ch + 64 * u;
-                        v4i_g x = staged ? *(const v4i_g *)(sv + xc * 16)
-                                         : *(const v4i_g *)(vec + j * vld_b + (ch + 64 * u) * 16);
+                    const v4i_g xv = xchunk(j, ch + 64 * u);
 #pragma unroll
-                        for (int r = 0; r < RPW; ++r) acc[r][j] = D::dot(m[u][r], x, acc[r][j]);
-                    }
+                    for (int r = 0; r < RPW; ++r) acc[r][j] = D::dot(m[u][r], xv, acc[r][j]);
                 }
-            }
         }
         for (; ch < nch; ch += 64) {
-            v4i_g m[RPW];
-#pragma unroll
-            for (int r = 0; r < RPW; ++r) m[r] = *(const v4i_g *)(rowp[r] + ch * 16);
 #pragma unroll
             for (int j = 0; j < NV; ++j) {
-                if (j < nvec) {
-                    v4i_g x = staged ? *(const v4i_g *)(sv + (j * nch + ch) * 16)
-                                     : *(const v4i_g *)(vec + j * vld_b + ch * 16);
+                const v4i_g xv = xchunk(j, ch);
 #pragma unroll
-                    for (int r = 0; r < RPW; ++r) acc[r][j] = D::dot(m[r], x, acc[r][j]);
-                }
+                for (int r = 0; r < RPW; ++r)
+                    acc[r][j] = D::dot(*(const v4i_g *)(rowp[r] + ch * 16), xv, acc[r][j]);
             }
         }
+        acc_t v[RPW * NV];
 #pragma unroll
-        for (int r = 0; r < RPW; ++r) {
+        for (int r = 0; r < RPW; ++r)
 #pragma unroll
-            for (int j = 0; j < NV; ++j) {
-                if (j < nvec) {
-                    acc_t v = D::reduce(acc[r][j]);
-                    if (lane == j && rok[r]) Store<E>::apply(ep, 0, j, (int)(r0 + r), v);
-                }
-            }
-        }
+            for (int j = 0; j < NV; ++j) v[r * NV + j] = acc[r][j];
+        wave_reduce(v);
+        store_group<T, E, NV, RPW>(g, ep, r0, v);
     }
 }
 
-template <InType T, EpiKind E, int NV>
-static hipError_t gemv_go(const GemvArgs &g, const EpiParams &ep, hipStream_t stream) {
-    constexpr int RPW = (NV <= 2) ? 4 : 2;
-    const int esz = (T == InType::I8) ? 1 : (T == InType::BF16 ? 2 : 4);
-    int64_t vbytes = (int64_t)g.nvec * (((int64_t)g.K * esz + 15) / 16) * 16;
-    size_t shm = vbytes <= kGemvLdsMax ? (size_t)vbytes : 0;
-    int64_t waves_needed = (g.R + RPW - 1) / RPW;
-    int64_t blocks = (waves_needed + kGemvWaves - 1) / kGemvWaves;
-    // Cap the grid so staging the vectors stays a small fraction of the traffic.
-    const int64_t cap = 256 * 8;
+// Persistent grid: enough workgroups to cover the row groups, at most
+// `per_cu` per CU.
+static unsigned gemv_grid(int64_t groups, int cus, int per_cu) {
+    int64_t blocks = (groups + kGemvWaves - 1) / kGemvWaves;
+    const int64_t cap = (int64_t)(cus > 0 ? cus : 256) * per_cu;
     if (blocks > cap) blocks = cap;
-    if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL((gemv_kernel<T, E, NV, RPW>), dim3((unsigned)blocks), dim3(kGemvThreads),
-                       shm, stream, g, ep);
+    return (unsigned)(blocks < 1 ? 1 : blocks);
+}
+
+// Rows per wave iteration: about 16 chunk loads per lane in flight behind the
+// arithmetic, at most 4 rows, and 2 when 8 vectors already fill the registers.
+template <int NV, int CPL>
+constexpr int rows_per_wave() {
+    return (CPL >= 8 || (NV >= 8 && CPL >= 4)) ? 2 : 4;
+}
+
+template <InType T, EpiKind E, int NV, int CPL>
+static hipError_t go_reg(const GemvArgs &g, const EpiParams &ep, hipStream_t stream) {
+    constexpr int RPW = rows_per_wave<NV, CPL>();
+    const int64_t groups = ((int64_t)g.R + RPW - 1) / RPW;
+    hipLaunchKernelGGL((gemv_reg<T, E, NV, CPL, RPW>), dim3(gemv_grid(groups, g.cus, 8)),
+                       dim3(kGemvThreads), 0, stream, g, ep);
     return hipGetLastError();
+}
+
+template <InType T, EpiKind E, int NV>
+static hipError_t go_lds(const GemvArgs &g, const EpiParams &ep, hipStream_t stream) {
+    constexpr int RPW = NV <= 2 ? 2 : 1;
+    constexpr int esz = (T == InType::I8) ? 1 : (T == InType::BF16 ? 2 : 4);
+    const int64_t vbytes = (int64_t)NV * (((int64_t)g.K * esz + 15) / 16) * 16;
+    const size_t shm = vbytes <= kGemvLdsMax ? (size_t)vbytes : 0;
+    const int64_t groups = ((int64_t)g.R + RPW - 1) / RPW;
+    hipLaunchKernelGGL((gemv_lds<T, E, NV, RPW>), dim3(gemv_grid(groups, g.cus, 2)),
+                       dim3(kGemvThreads), shm, stream, g, ep);
+    return hipGetLastError();
+}
+
+// Register-resident vectors while NV x CPL chunks per lane stay within the
+// register budget (bf16 needs extra registers to widen its operands).
+template <InType T, int NV, int CPL>
+constexpr bool reg_fits() {
+    return NV * CPL <= (T == InType::BF16 ? 16 : 32);
+}
+
+template <InType T, EpiKind E, int NV>
+static hipError_t go_nv(const GemvArgs &g, const EpiParams &ep, hipStream_t stream) {
+    constexpr int esz = (T == InType::I8) ? 1 : (T == InType::BF16 ? 2 : 4);
+    const int64_t nch = ((int64_t)g.K * esz + 15) / 16;
+    if (nch <= 64) return go_reg<T, E, NV, 1>(g, ep, stream);
+    if (nch <= 128) return go_reg<T, E, NV, 2>(g, ep, stream);
+    if constexpr (reg_fits<T, NV, 4>())
+        if (nch <= 256) return go_reg<T, E, NV, 4>(g, ep, stream);
+    if constexpr (reg_fits<T, NV, 8>())
+        if (nch <= 512) return go_reg<T, E, NV, 8>(g, ep, stream);
+    return go_lds<T, E, NV>(g, ep, stream);
 }
 
 template <InType T, EpiKind E>
 static hipError_t gemv_nv(const GemvArgs &g, const EpiParams &ep, hipStream_t stream) {
-    if (g.nvec <= 1) return gemv_go<T, E, 1>(g, ep, stream);
-    if (g.nvec <= 2) return gemv_go<T, E, 2>(g, ep, stream);
-    if (g.nvec <= 4) return gemv_go<T, E, 4>(g, ep, stream);
-    return gemv_go<T, E, 8>(g, ep, stream);
+    if (g.nvec <= 1) return go_nv<T, E, 1>(g, ep, stream);
+    if (g.nvec <= 2) return go_nv<T, E, 2>(g, ep, stream);
+    if (g.nvec <= 4) return go_nv<T, E, 4>(g, ep, stream);
+    return go_nv<T, E, 8>(g, ep, stream);
 }
 
 hipError_t launch_gemv(InType in, const GemvArgs &g, const EpiParams &ep, hipStream_t stream) {
-    if (g.nvec < 1 || g.nvec > 8) return hipErrorInvalidValue;
+    if (g.nvec < 1 || g.nvec > 8 || g.R < 1) return hipErrorInvalidValue;
     switch (in) {
     case InType::I8:
         if (ep.kind == EpiKind::I32) return gemv_nv<InType::I8, EpiKind::I32>(g, ep, stream);

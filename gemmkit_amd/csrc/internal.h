@@ -39,8 +39,9 @@ struct EpiParams {
     int32_t vec4;          // C is unit-stride along columns and 4-element aligned
 };
 
-// Largest operand row stride (bytes) the matrix-core kernels address: 256 rows
-// of a tile stay below 2^31 bytes of 32-bit buffer offsets.
+// Largest operand row stride and row length (bytes) the matrix-core kernels
+// address: 256 row strides plus a row stay below 2^31 bytes of 32-bit buffer
+// offsets.
 constexpr int64_t kMaxTileRowBytes = 0x7FFFFFF0 / 256;
 
 struct MmaArgs {
@@ -73,10 +74,17 @@ struct GemvArgs {
     const void *vec;       // nvec x K, k-contiguous, vld apart
     int64_t vld;
     int32_t R, K, nvec;
+    int32_t cus;           // compute units of the device (persistent grid size)
     // Output element (vector j, matrix row r) is stored as the epilogue's
     // (row j, column r): at c + j*rsc + r*csc of the EpiParams.
 };
 hipError_t launch_gemv(InType in, const GemvArgs &g, const EpiParams &ep, hipStream_t stream);
+
+// Matrix-core skinny route (1..16 vectors): the vectors are staged in LDS,
+// which must hold skinny_lds_bytes() <= kSkinnyLdsMax.
+constexpr int64_t kSkinnyLdsMax = 64 * 1024;
+int64_t skinny_lds_bytes(InType in, int64_t K, int nvec);
+hipError_t launch_skinny(InType in, const GemvArgs &g, const EpiParams &ep, hipStream_t stream);
 
 // Pack a strided rows x K operand into a k-contiguous buffer with row stride
 // ld (>= K, ld*esize a multiple of 16); columns [K, ld) are zero-filled.

@@ -111,6 +111,7 @@ constexpr int kSchedVmem = 0x010;
 // kMaxRecords, which the host guarantees for every in-range byte of a tile.
 constexpr uint32_t kMaxRecords = 0x7FFFFFF0u;
 constexpr uint32_t kOutOfRange = 0x80000000u;
+static_assert(kOutOfRange > kMaxRecords, "out-of-range offset must exceed every resource size");
 constexpr int kRsrcWord3 = 0x00020000;  // raw (unswizzled) buffer, 32-bit data format
 
 // One direct-to-LDS load of 16 bytes per lane: lane l reads base[voff] into
@@ -164,15 +165,19 @@ __device__ __forceinline__ void stage_barrier() {
 // Epilogue: each wave stages 32 accumulator rows at a time through LDS and
 // writes them back as row-contiguous 4-element chunks (16-byte stores for
 // i32/f32 output).
-template <int BM, int BN, int WM, int WN>
+// Register budget: the waves of as many workgroups as the 160 KiB of LDS
+// holds (at most two), spread over the CU's 4 SIMDs.
+template <int BM, int BN, int WM, int WN, int BK, int NS>
 constexpr int waves_per_simd() {
-    return (WM * WN > 4 || BM * BN < 256 * 256) ? 2 : 1;
+    constexpr int smem = NS * (BM + BN) * BK;
+    constexpr int wgs = smem * 2 <= 160 * 1024 ? 2 : 1;
+    return wgs * WM * WN / 4 > 1 ? wgs * WM * WN / 4 : 1;
 }
 
 template <InType T, EpiKind E, int BM, int BN, int WM, int WN, int BK, int NS>
 __global__ __launch_bounds__(WM * WN * 64)
-__attribute__((amdgpu_waves_per_eu(waves_per_simd<BM, BN, WM, WN>(),
-                                   waves_per_simd<BM, BN, WM, WN>())))
+__attribute__((amdgpu_waves_per_eu(waves_per_simd<BM, BN, WM, WN, BK, NS>(),
+                                   waves_per_simd<BM, BN, WM, WN, BK, NS>())))
 void mma_kernel(const MmaArgs args, const EpiParams ep) {
     constexpr int NWAVES = WM * WN;
     constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -215,11 +220,15 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     const bool k_whole = (kbytes % BK) == 0;
 
     // The tile's A rows [m0, m0+BM) and B rows [n0, n0+BN) as two buffer
-    // resources; rows past the matrix edge fall outside them and read zeros.
+    // resources spanning the valid rows' bytes (rows may overlap: a stride
+    // below the row length is a legal view).  Rows past the matrix edge start
+    // outside them and read zeros, or, with overlapping rows, feed outputs
+    // that are never stored.
+    const int64_t kb16 = (kbytes + 15) / 16 * 16;
     const uint8_t *a_pan = A + (int64_t)m0 * lda_b;
     const uint8_t *b_pan = B + (int64_t)n0 * ldb_b;
-    const uint32_t a_num = (uint32_t)((args.M - m0 < BM ? args.M - m0 : BM) * lda_b);
-    const uint32_t b_num = (uint32_t)((args.N - n0 < BN ? args.N - n0 : BN) * ldb_b);
+    const uint32_t a_num = (uint32_t)(((args.M - m0 < BM ? args.M - m0 : BM) - 1) * lda_b + kb16);
+    const uint32_t b_num = (uint32_t)(((args.N - n0 < BN ? args.N - n0 : BN) - 1) * ldb_b + kb16);
 
     // This lane's source chunk for each of the wave's NIW load instructions:
     // instruction q fills stage bytes [q*1024, q*1024 + 1024), lane l the 16

@@ -135,3 +135,20 @@ def test_4096_cube_benchmark_shape(dev):
     colsum = oracle.colsum_i32(M, N, got, N, 1)
     abft = oracle.abft_i8(M, K, N, a, K, 1, b, 1, K)
     assert np.array_equal(colsum, abft)
+
+
+@pytest.mark.parametrize("m,k,n", [(300, 64, 200), (5, 96, 300), (300, 128, 9)])
+def test_overlapping_rows(dev, m, k, n):
+    """A read-only view whose rows overlap (row stride 16 < K): legal for A and
+    B (only C is checked for self-aliasing, src/api.rs:236-250)."""
+    import torch
+    rsa, csa = 16, 1
+    alen = (m - 1) * rsa + k
+    a = oracle.rand_i8_100(0x3300 + m, alen)
+    b = oracle.rand_i8_100(0x3400 + n, k * n)
+    want = np.zeros(m * n, np.int32)
+    oracle.gemm_i8(m, k, n, 1, a, rsa, csa, b, 1, k, 0, want, n, 1)
+    c = torch.empty(m * n, dtype=torch.int32, device=dev)
+    gk.gemm_i8(1, gk.MatRef(to_dev(a, dev), m, k, rsa, csa), gk.MatRef(to_dev(b, dev), k, n, 1, k),
+               0, gk.MatMut.from_row_major(c, m, n))
+    assert np.array_equal(c.cpu().numpy(), want)
