@@ -324,7 +324,7 @@ Tile env_tile(bool *forced) {
     return Tile::T256x256;
 }
 
-// GEMMKIT_HIP_SKINNY=0 keeps products with a short side of 1..8 on the
+// GEMMKIT_HIP_SKINNY=0 keeps products with a short side of 2..8 on the
 // wavefront-reduction GEMV instead of the matrix-core skinny kernel.
 bool skinny_enabled() {
     const char *s = getenv("GEMMKIT_HIP_SKINNY");
@@ -409,7 +409,10 @@ int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t
     // its first row: 256 row strides plus a row must stay below 2 GiB.
     const bool offsets_fit = std::max(A.rs, Bt.rs) * (int64_t)esz <= kMaxTileRowBytes &&
                              k * (int64_t)esz <= kMaxTileRowBytes;
-    const bool skinny_ok = short_side <= 16 && skinny_enabled() && offsets_fit &&
+    // One vector streams best with the wavefront GEMV (a whole 1 KiB row
+    // segment per load, no cross-wave exchange); 2..16 vectors go to the
+    // matrix-core kernel.
+    const bool skinny_ok = short_side >= 2 && short_side <= 16 && skinny_enabled() && offsets_fit &&
                            skinny_lds_bytes(in, k, (int)short_side) <= kSkinnyLdsMax;
     if (skinny_ok || short_side <= 8) {
         // Skinny route: the short side's rows are the vectors, streamed

@@ -7,20 +7,25 @@
 // 16: out[j, r] = epi( sum_p mat[r, p] * vec[j, p] ), r < R, j < nvec.
 //
 // Layout on the matrix cores: v_mfma_*_16x16x(64 i8 | 32 bf16 | 4x4 f32) with
-// the matrix rows as the instruction's 16 rows and the (zero-padded) vectors
-// as its 16 columns.  Lane l supplies row l%16 and vector l%16 with the 16
-// bytes at k offset 16*(l/16) of each 64-byte k step, so every load
-// instruction reads 16 rows x 64 contiguous bytes of the matrix.  The vectors
-// are staged once per workgroup in LDS (row stride padded so the 16 lanes of
-// an LDS cycle hit distinct banks); the matrix goes global -> VGPRs through a
-// buffer resource (rows past R and bytes past K read as zeros).
+// the (zero-padded) vectors as the instruction's 16 columns.  A load
+// instruction reads 8 matrix rows x 128 contiguous bytes (a 128-byte k step):
+// lane l (i = l%16, g = l/16) takes row i/2 of the 8, chunk c = 2g + i%2.  As
+// MFMA operand, lane l is instruction row i with k group g, so row i pairs
+// chunk 2g + i%2 of its matrix row with whatever chunk the vector operand
+// holds for group g.  Two MFMAs per load, one with vector chunks 2g (h = 0)
+// and one with 2g + 1 (h = 1), make the products of the even rows exact in
+// the first and of the odd rows in the second; the other halves are ignored.
+// Result (16x16 accumulator: register q of lane l is instruction row
+// 4*(l/16) + q, vector l%16): matrix row 2*(l/16) + e of the block is
+// acc_h0[2e] + acc_h1[2e+1], a per-lane add.  The vectors are staged once per
+// workgroup in LDS (row stride padded so the 16 lanes of an LDS cycle hit
+// distinct banks); the matrix goes global -> VGPRs through a buffer resource
+// (rows past R and bytes past K read as zeros).
 //
-// Work item: 32 matrix rows (two 16-row blocks) x all of K.  The 4 waves of a
-// workgroup split K into 4 contiguous ranges; each keeps 8 k steps x 2 blocks
-// (16 KiB) of loads in flight behind its MFMAs, and the four partial 16x16
-// blocks are summed through LDS, in wave order, before the epilogue.
-// Accumulator layout (16x16 block): register r of lane l holds matrix row
-// 4*(l/16) + r, vector l%16.
+// Work item: 32 matrix rows (four 8-row blocks) x all of K.  The 4 waves of a
+// workgroup split K into 4 contiguous ranges; each keeps 4 k steps x 4 blocks
+// (16 KiB) of loads in flight behind its MFMAs, and the four partial sums are
+// added through LDS, in wave order, before the epilogue.
 #include "epilogue.h"
 
 namespace gk {
@@ -67,10 +72,11 @@ struct Mma16<InType::F32> {
 
 constexpr int kSkThreads = 256;
 constexpr int kSkWaves = 4;
-constexpr int kSkRB = 2;                   // 16-row blocks per work item
-constexpr int kSkRows = 16 * kSkRB;        // matrix rows per work item
-constexpr int kSkPF = 8;                   // k steps per load batch
-constexpr int kSkCombine = kSkWaves * kSkRB * 4 * 64 * 4;  // partial-sum exchange bytes
+constexpr int kSkBlocks = 4;               // 8-row blocks per work item
+constexpr int kSkRows = 8 * kSkBlocks;     // matrix rows per work item
+constexpr int kSkStep = 128;               // k bytes per step (one load per block)
+constexpr int kSkPF = 4;                   // k steps per load batch
+constexpr int kSkCombine = kSkWaves * kSkBlocks * 2 * 64 * 4;  // partial-sum exchange bytes
 constexpr uint32_t kSkOut = 0x80000000u;   // out-of-range buffer offset (reads zeros)
 constexpr int kSkRsrcWord3 = 0x00020000;   // raw buffer, 32-bit data format
 
@@ -98,94 +104,129 @@ __global__ __launch_bounds__(kSkThreads) void skinny_mfma(const GemvArgs g, cons
     // multiple of 16 only arrives through the pack, which zero-fills both
     // operands' rows up to the next 16 bytes.
     const int64_t kb = ((int64_t)g.K * esz + 15) / 16 * 16;
-    const int nk = (int)((kb + 63) / 64);
+    const int nk = (int)((kb + kSkStep - 1) / kSkStep);
     const int64_t xs = skinny_xstride(kb);
     const int nvec = g.nvec;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-    // Stage the vectors: nvec rows of kb bytes.
-    const uint8_t *vec = (const uint8_t *)g.vec;
-    const int64_t vld_b = g.vld * esz, cpr = kb / 16;
-    for (int64_t c = tid; c < nvec * cpr; c += kSkThreads) {
-        const int64_t j = c / cpr, q = c % cpr;
-        *(v4i_s *)(sh + j * xs + q * 16) = *(const v4i_s *)(vec + j * vld_b + q * 16);
-    }
-    val_t *comb = (val_t *)(sh + nvec * xs);
-    __syncthreads();
-
-    const int lrow = lane & 15, lgrp = lane >> 4;
-    const bool lvec = lrow < nvec;
-    const int64_t xaddr = (int64_t)(lvec ? lrow : 0) * xs + lgrp * 16;
+    const int li = lane & 15, lg = lane >> 4;
+    const int chunk = 2 * lg + (li & 1);      // this lane's 16-byte chunk of a k step
+    const bool lvec = li < nvec;
+    const int64_t xaddr = (int64_t)(lvec ? li : 0) * xs + 32 * lg;  // + 16*h for MFMA h
     const int kseg = (nk + kSkWaves - 1) / kSkWaves;
     const int ks0 = wave * kseg, ks1 = ks0 + kseg < nk ? ks0 + kseg : nk;
 
+    // This wave's load batches, in order: for each of the workgroup's items
+    // (blockIdx.x, + gridDim.x, ...), nbw batches of kSkPF k steps of its K
+    // range (at least one, all out of range when the range is empty, so every
+    // wave takes part in every item's exchange).  Two register buffers
+    // alternate: batch t+1 is in flight while batch t is multiplied, across
+    // item boundaries too.
     const uint8_t *mat = (const uint8_t *)g.mat;
     const int64_t ld_b = g.ld * esz;
     const int items = (g.R + kSkRows - 1) / kSkRows;
-    for (int item = blockIdx.x; item < items; item += gridDim.x) {
-        const int r0 = item * kSkRows;
+    const int my_items = (int)blockIdx.x < items ? (items - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+    const int nbw = ks1 > ks0 ? (ks1 - ks0 + kSkPF - 1) / kSkPF : 1;
+    const int total = my_items * nbw;
+    uint32_t off[kSkBlocks];
+#pragma unroll
+    for (int b = 0; b < kSkBlocks; ++b) off[b] = (uint32_t)((8 * b + (li >> 1)) * ld_b + 16 * chunk);
+    auto issue = [&](int t, v4i_s (&m)[kSkPF][kSkBlocks]) {
+        const int r0 = ((int)blockIdx.x + (t / nbw) * (int)gridDim.x) * kSkRows;
+        const int s0 = ks0 + (t % nbw) * kSkPF;
         const uint8_t *base = mat + (int64_t)r0 * ld_b;
         // Extent of the item's valid rows (rows may overlap: ld_b < kb is a
         // legal view); rows past R read zeros when they start past it and
         // otherwise produce outputs that are never stored.
         const int nrows = g.R - r0 < kSkRows ? g.R - r0 : kSkRows;
         const uint32_t num = (uint32_t)((nrows - 1) * ld_b + kb);
-        uint32_t off[kSkRB];
 #pragma unroll
-        for (int b = 0; b < kSkRB; ++b) off[b] = (uint32_t)((b * 16 + lrow) * ld_b + lgrp * 16);
+        for (int p = 0; p < kSkPF; ++p) {
+            const int s = s0 + p;
+            const bool in = s < ks1 && (int64_t)s * kSkStep + 16 * chunk < kb;
+#pragma unroll
+            for (int b = 0; b < kSkBlocks; ++b)
+                m[p][b] = load16(base, num, in ? off[b] + (uint32_t)s * kSkStep : kSkOut);
+        }
+    };
+    v4i_s buf0[kSkPF][kSkBlocks], buf1[kSkPF][kSkBlocks];
+    if (total > 0) issue(0, buf0);  // in flight while the vectors are staged
 
-        auto load_batch = [&](int s0, v4i_s (&m)[kSkPF][kSkRB]) {
+    // Stage the vectors: nvec rows of kb bytes, 8 chunks per thread in flight
+    // at a time (one L2 round trip for up to 32 KiB).
+    const uint8_t *vec = (const uint8_t *)g.vec;
+    const int64_t vld_b = g.vld * esz, cpr = kb / 16, nchunks = nvec * cpr;
+    for (int64_t c0 = tid; c0 < nchunks; c0 += kSkThreads * 8) {
+        v4i_s tmp[8];
 #pragma unroll
-            for (int p = 0; p < kSkPF; ++p) {
-                const int s = s0 + p;
-                const bool in = s < ks1 && (int64_t)s * 64 + lgrp * 16 < kb;
+        for (int u = 0; u < 8; ++u) {
+            const int64_t c = c0 + (int64_t)u * kSkThreads;
+            tmp[u] = c < nchunks ? *(const v4i_s *)(vec + (c / cpr) * vld_b + (c % cpr) * 16)
+                                 : v4i_s{0, 0, 0, 0};
+        }
 #pragma unroll
-                for (int b = 0; b < kSkRB; ++b)
-                    m[p][b] = load16(base, num, in ? off[b] + (uint32_t)s * 64 : kSkOut);
-            }
-        };
+        for (int u = 0; u < 8; ++u) {
+            const int64_t c = c0 + (int64_t)u * kSkThreads;
+            if (c < nchunks) *(v4i_s *)(sh + (c / cpr) * xs + (c % cpr) * 16) = tmp[u];
+        }
+    }
+    val_t *comb = (val_t *)(sh + nvec * xs);
+    __syncthreads();
 
-        acc_t acc[kSkRB];
+    acc_t acc[2][kSkBlocks];
+    // Multiplies batch t; after an item's last batch, forms each matrix row's
+    // result from the two MFMAs, sums the four K ranges (wave order) through
+    // LDS and applies the epilogue.
+    auto run = [&](int t, const v4i_s (&m)[kSkPF][kSkBlocks]) {
+        const int q = t % nbw;
+        if (q == 0) {
 #pragma unroll
-        for (int b = 0; b < kSkRB; ++b) acc[b] = acc_t{};
-        v4i_s cur[kSkPF][kSkRB], nxt[kSkPF][kSkRB];
-        if (ks0 < ks1) load_batch(ks0, nxt);
-        for (int s0 = ks0; s0 < ks1; s0 += kSkPF) {
+            for (int b = 0; b < kSkBlocks; ++b) acc[0][b] = acc[1][b] = acc_t{};
+        }
+        const int s0 = ks0 + q * kSkPF;
 #pragma unroll
-            for (int p = 0; p < kSkPF; ++p)
+        for (int p = 0; p < kSkPF; ++p) {
+            const int s = s0 + p;
+            if (s < ks1) {
 #pragma unroll
-                for (int b = 0; b < kSkRB; ++b) cur[p][b] = nxt[p][b];
-            if (s0 + kSkPF < ks1) load_batch(s0 + kSkPF, nxt);
+                for (int h = 0; h < 2; ++h) {
+                    v4i_s xv = *(const v4i_s *)(sh + xaddr + (int64_t)s * kSkStep + 16 * h);
+                    if (!lvec || (int64_t)s * kSkStep + 16 * (2 * lg + h) >= kb) xv = v4i_s{0, 0, 0, 0};
 #pragma unroll
-            for (int p = 0; p < kSkPF; ++p) {
-                const int s = s0 + p;
-                if (s < ks1) {
-                    v4i_s xv = *(const v4i_s *)(sh + xaddr + (int64_t)s * 64);
-                    if (!lvec || (int64_t)s * 64 + lgrp * 16 >= kb) xv = v4i_s{0, 0, 0, 0};
-#pragma unroll
-                    for (int b = 0; b < kSkRB; ++b) acc[b] = Mm::step(cur[p][b], xv, acc[b]);
+                    for (int b = 0; b < kSkBlocks; ++b) acc[h][b] = Mm::step(m[p][b], xv, acc[h][b]);
                 }
             }
         }
-
-        // Sum the four K ranges (wave order) and apply the epilogue.
+        if (q != nbw - 1) return;
+        const int r0 = ((int)blockIdx.x + (t / nbw) * (int)gridDim.x) * kSkRows;
 #pragma unroll
-        for (int b = 0; b < kSkRB; ++b)
+        for (int b = 0; b < kSkBlocks; ++b)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) comb[((wave * kSkRB + b) * 4 + r) * 64 + lane] = (val_t)acc[b][r];
+            for (int e = 0; e < 2; ++e)
+                comb[((wave * kSkBlocks + b) * 2 + e) * 64 + lane] =
+                    (val_t)acc[0][b][2 * e] + (val_t)acc[1][b][2 * e + 1];
         __syncthreads();
+        constexpr int kPer = kSkBlocks * 2 / kSkWaves;  // 64-entry rows each wave sums
 #pragma unroll
-        for (int t = 0; t < kSkRB * 4 / kSkWaves; ++t) {
-            const int e = (wave * (kSkRB * 4 / kSkWaves) + t) * 64 + lane;  // over kSkRB*4*64
-            const int b = e / 256, r = (e / 64) % 4, ln = e % 64;
-            val_t sum = comb[e];
+        for (int u = 0; u < kPer; ++u) {
+            const int x = (wave * kPer + u) * 64 + lane;  // over kSkBlocks*2*64
+            const int b = x / 128, e = (x / 64) % 2, ln = x % 64;
+            val_t sum = comb[x];
 #pragma unroll
-            for (int w = 1; w < kSkWaves; ++w) sum += comb[w * kSkRB * 4 * 64 + e];
-            const int row = r0 + b * 16 + 4 * (ln / 16) + r, j = ln % 16;
+            for (int w = 1; w < kSkWaves; ++w) sum += comb[w * kSkBlocks * 2 * 64 + x];
+            const int row = r0 + 8 * b + 2 * (ln >> 4) + e, j = ln & 15;
             if (j < nvec && row < g.R) Store<E>::apply(ep, 0, j, row, sum);
         }
         __syncthreads();
+    };
+    for (int t = 0; t < total; t += 2) {
+        if (t + 1 < total) issue(t + 1, buf1);
+        run(t, buf0);
+        if (t + 1 < total) {
+            if (t + 2 < total) issue(t + 2, buf0);
+            run(t + 1, buf1);
+        }
     }
 }
 
@@ -199,8 +240,10 @@ template <InType T, EpiKind E>
 static hipError_t skinny_go(const GemvArgs &g, const EpiParams &ep, hipStream_t stream) {
     const int64_t shm = skinny_lds_bytes(T, g.K, g.nvec);
     const int64_t items = (g.R + kSkRows - 1) / kSkRows;
-    const int per_cu = (int)(kSkinnyLdsMax / shm) < 4 ? (int)(kSkinnyLdsMax / shm) : 4;
-    int64_t blocks = (int64_t)(g.cus > 0 ? g.cus : 256) * (per_cu > 1 ? per_cu : 1);
+    // As many resident workgroups per CU as its 160 KiB of LDS holds (<= 4).
+    const int fit = (int)(160 * 1024 / shm);
+    const int per_cu = fit < 4 ? (fit > 1 ? fit : 1) : 4;
+    int64_t blocks = (int64_t)(g.cus > 0 ? g.cus : 256) * per_cu;
     if (blocks > items) blocks = items;
     hipLaunchKernelGGL((skinny_mfma<T, E>), dim3((unsigned)blocks), dim3(kSkThreads), (size_t)shm,
                        stream, g, ep);

@@ -1,7 +1,7 @@
 """GPU parity for the skinny route (products with a short side of 1..16).
 
-These shapes run on the matrix-core skinny kernel (vectors staged in LDS) or,
-with GEMMKIT_HIP_SKINNY=0 and a short side of at most 8, on the
+Short sides of 2..16 run on the matrix-core skinny kernel (vectors staged in
+LDS); a short side of 1, or up to 8 with GEMMKIT_HIP_SKINNY=0, runs on the
 wavefront-reduction GEMV.  i8 and requantized outputs are bit-exact against
 the oracle and identical between the two kernels; f32 and bf16 meet the
 tolerances of the float suite.  Includes the decode-shaped workload at full
@@ -23,7 +23,7 @@ pytestmark = pytest.mark.gpu
 
 
 class no_skinny:
-    """Context: route short sides <= 8 to the wavefront GEMV instead."""
+    """Context: route short sides 2..8 to the wavefront GEMV instead."""
 
     def __enter__(self):
         os.environ["GEMMKIT_HIP_SKINNY"] = "0"
@@ -53,7 +53,7 @@ def test_i8_skinny_layouts(dev, m, k, n, la, lb, lc):
     run_case(dev, m, k, n, 2, 1, la, lb, lc, seed=12)
 
 
-@pytest.mark.parametrize("m,k,n", [(1, 4096, 777), (8, 4096, 1000), (6, 4112, 300),
+@pytest.mark.parametrize("m,k,n", [(2, 4096, 777), (8, 4096, 1000), (6, 4112, 300),
                                    (500, 1040, 3)])
 def test_i8_skinny_matches_gemv(dev, m, k, n):
     """Both skinny kernels give identical bits (wrapping i32 sums)."""
