@@ -9,7 +9,8 @@ import ctypes as C
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libgemmkit_hip.so")
+# GEMMKIT_HIP_LIBRARY names another build of the same ABI (A/B comparisons).
+LIB_PATH = os.environ.get("GEMMKIT_HIP_LIBRARY") or os.path.join(_HERE, "libgemmkit_hip.so")
 
 _size = C.c_size_t
 _sdiff = C.c_ssize_t

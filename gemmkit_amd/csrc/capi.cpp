@@ -331,27 +331,32 @@ bool skinny_enabled() {
     return !(s && !strcmp(s, "0"));
 }
 
-// Tile table: per shape, the tile that minimises waves x per-wave work, where
-// a CU holds `occ` workgroups of a tile at once and `eff` is the tile's
-// relative matrix-core efficiency.
+// Tile choice: the tile with the smallest makespan.  Tiles spread evenly over
+// the CUs, so the busiest CU runs ceil(tiles / CUs) of them, up to `occ` at a
+// time; a CU running n tiles of BM x BN together delivers eff[n-1] of its
+// matrix-core peak.  The efficiencies are measured cycles per K stage of
+// each tile against its MFMA-bound cycles (4096^3 and 2048 x 11008 x 4096
+// int8 runs); small tiles lose most to load issue and the stage barrier.
 Tile pick_tile(int64_t M, int64_t N, int64_t batch) {
     bool forced;
     Tile t = env_tile(&forced);
     if (forced) return t;
-    struct Cand { Tile t; int bm, bn, occ; double eff; };
+    struct Cand { Tile t; int bm, bn, occ; double eff[2]; };
     static const Cand cands[] = {
-        {Tile::T256x256, 256, 256, 1, 1.00},
-        {Tile::T256x128, 256, 128, 1, 0.90},
-        {Tile::T128x128, 128, 128, 2, 0.75},
-        {Tile::T64x64, 64, 64, 4, 0.40},
+        {Tile::T256x256, 256, 256, 1, {0.83, 0.83}},
+        {Tile::T256x128o2, 256, 128, 2, {0.45, 0.60}},
+        {Tile::T256x128, 256, 128, 1, {0.55, 0.55}},
+        {Tile::T128x128, 128, 128, 2, {0.35, 0.50}},
+        {Tile::T64x64, 64, 64, 2, {0.20, 0.30}},
     };
     double best = 1e300;
     Tile bt = Tile::T64x64;
+    const int64_t cus = g_num_cus > 0 ? g_num_cus : 256;
     for (const Cand &c : cands) {
-        int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * batch;
-        int64_t slots = (int64_t)g_num_cus * c.occ;
-        int64_t waves = (tiles + slots - 1) / slots;
-        double cost = (double)waves * c.occ * c.bm * c.bn / c.eff;
+        const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * batch;
+        const int64_t per_cu = (tiles + cus - 1) / cus;
+        const int together = (int)std::min<int64_t>(per_cu, c.occ);
+        const double cost = (double)per_cu * c.bm * c.bn / c.eff[together - 1];
         if (cost < best * 0.999) { best = cost; bt = c.t; }
     }
     return bt;

@@ -11,10 +11,12 @@
 //        src/simd/avx512.rs:194-212;
 //   Q8   KRequantize::apply (src/kernel/epilogue.rs:810-830): wrapping bias add,
 //        one f64 multiply by the widened f32 scale, round half to even, zero
-//        point, clamp to [lo, hi], store the low byte.
+//        point, clamp to [lo, hi], store the low byte -- computed exactly
+//        without f64 arithmetic (requant.h).
 #pragma once
 
 #include "internal.h"
+#include "requant.h"
 
 namespace gk {
 
@@ -29,22 +31,13 @@ __device__ __forceinline__ float bf16_widen(uint16_t h) {
     return __uint_as_float((uint32_t)h << 16);
 }
 
-// The requant map on one i32 accumulator.  The product of an i32 and an f32,
-// both exact in f64, is one IEEE multiply; rint() is round-half-to-even under
-// the default rounding mode, and is the identity for |x| >= 2^52 exactly like
-// round_ne_f64's pass-through (src/kernel/epilogue.rs:886-897).  Adding zp in
-// f64 and clamping there equals the reference's saturating i64 add and clamp:
-// below 2^52 the sum is exact, above it both clamp to the band edge.
+// The requant map on one i32 accumulator (requant.h): f32 arithmetic with an
+// exact tie correction for operands below 2^24, 64-bit integer arithmetic
+// otherwise; bit-identical to the f64 formula either way, without CDNA4's
+// slow f64 VALU ops.
 __device__ __forceinline__ int32_t requant_value(int32_t acc, int32_t bias, float scale,
                                                  int32_t zp, int32_t lo, int32_t hi) {
-#pragma clang fp contract(off)
-    int32_t v = (int32_t)((uint32_t)acc + (uint32_t)bias);
-    double x = (double)v * (double)scale;
-    double r = __builtin_rint(x);
-    r = r + (double)zp;
-    r = __builtin_fmax(r, (double)lo);
-    r = __builtin_fmin(r, (double)hi);
-    return (int32_t)r;
+    return requant_fast(acc, bias, scale, zp, lo, hi);
 }
 
 // Stores one accumulator at output coordinate (row, col) of batch element z.
@@ -115,13 +108,41 @@ struct Store<EpiKind::Q8> {
 // Four consecutive output columns (col .. col+3) of one row, from the
 // LDS-staged accumulators.  `vec` (uniform) says C is unit-stride along columns
 // and 4-element aligned, so whole chunks take one vector access; otherwise, and
-// for chunks that straddle the matrix edge, each element goes through Store.
+// for chunks that straddle the matrix edge, each element is stored alone.
+// Requantization uses the caller's per-element channel scale and bias (qs,
+// qb): the f32 path for all four, and the exact integer path for every lane
+// of the wave when any lane needs it.
 template <EpiKind K, typename A>
 __device__ __forceinline__ void store4(const EpiParams &ep, int64_t z, int row, int col, int ncols,
-                                       const A v[4]) {
+                                       const A v[4], const float *qs = nullptr,
+                                       const int32_t *qb = nullptr) {
     const int nvalid = ncols - col < 4 ? ncols - col : 4;
+    int32_t q[4] = {0, 0, 0, 0};
+    if constexpr (K == EpiKind::Q8) {
+        bool slow = false;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const RequantF32 r = requant_f32((int32_t)v[e], qb[e], qs[e], ep.zp, ep.lo, ep.hi);
+            q[e] = r.q;
+            slow = slow || r.slow;
+        }
+        if (__builtin_amdgcn_ballot_w64(slow) != 0) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                q[e] = requant_bits((int32_t)v[e], qb[e], __float_as_uint(qs[e]), ep.zp, ep.lo,
+                                    ep.hi);
+        }
+    }
     if (!ep.vec4 || nvalid < 4) {
-        for (int e = 0; e < nvalid; ++e) Store<K>::apply(ep, z, row, col + e, v[e]);
+        for (int e = 0; e < nvalid; ++e) {
+            if constexpr (K == EpiKind::Q8) {
+                uint8_t *c = (uint8_t *)ep.c + z * ep.bsc + (int64_t)row * ep.rsc +
+                             (int64_t)(col + e) * ep.csc;
+                *c = (uint8_t)(q[e] & 0xFF);
+            } else {
+                Store<K>::apply(ep, z, row, col + e, v[e]);
+            }
+        }
         return;
     }
     const int64_t off = z * ep.bsc + (int64_t)row * ep.rsc + col;
@@ -166,14 +187,8 @@ __device__ __forceinline__ void store4(const EpiParams &ep, int64_t z, int row, 
         o[1] = (uint32_t)bf16_rne(f[2]) | ((uint32_t)bf16_rne(f[3]) << 16);
         *c = o;
     } else {
-        uint32_t word = 0;
-        for (int e = 0; e < 4; ++e) {
-            int ch = ep.axis ? col + e : row;
-            float sc = ep.scales ? ep.scales[ch] : ep.scale;
-            int32_t b = ep.bias ? ep.bias[ch] : 0;
-            int32_t q = requant_value(v[e], b, sc, ep.zp, ep.lo, ep.hi);
-            word |= (uint32_t)(q & 0xFF) << (8 * e);
-        }
+        const uint32_t word = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
+                              ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)q[3] << 24);
         *(uint32_t *)((uint8_t *)ep.c + off) = word;
     }
 }

@@ -315,9 +315,39 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     // The empty asm statements pin F0 and F1 around the barrier so the compiler
     // keeps each phase's MFMAs on its side.
     constexpr int H0 = NIW / 2, H1 = NIW - H0;  // loads issued in phase A / C
+
+    // Requantization: the tile's channels (rows for a per-row map, columns
+    // for a per-column one) get their scale and bias staged in LDS, so the
+    // epilogue reads them without global loads.  They are loaded here, stay
+    // in flight behind the prologue's stage loads (loads complete in order),
+    // and reach LDS after the prologue wait; the main loop's barriers publish
+    // them.
+    constexpr int QCH = (E == EpiKind::Q8) ? (BM > BN ? BM : BN) : 1;
+    __shared__ float q_scale[QCH];
+    __shared__ int32_t q_bias[QCH];
+    static_assert(E != EpiKind::Q8 || QCH <= NWAVES * 64, "one channel per thread");
+    int q_ch0 = 0, q_n = 0;
+    float q_s = 0.0f;
+    int32_t q_b = 0;
+    if constexpr (E == EpiKind::Q8) {
+        q_n = ep.axis ? BN : BM;
+        q_ch0 = ep.axis ? n0 : m0;
+        const int lim = ep.axis ? args.N : args.M, ch = q_ch0 + tid;
+        if (tid < q_n) {
+            q_s = ep.scales ? (ch < lim ? ep.scales[ch] : 1.0f) : ep.scale;
+            q_b = (ep.bias && ch < lim) ? ep.bias[ch] : 0;
+        }
+    }
+
 #pragma unroll
     for (int s0 = 0; s0 < NS - 1; ++s0) issue_stage(s0, s0, 0, NIW);
     wait_vmcnt<(NS - 2) * NIW>();
+    if constexpr (E == EpiKind::Q8) {
+        if (tid < q_n) {
+            q_scale[tid] = q_s;
+            q_bias[tid] = q_b;
+        }
+    }
     stage_barrier();
     read_frags(smem, 0, 0);
 
@@ -364,6 +394,24 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     val_t *stg = (val_t *)smem + wave * 32 * EPI_LD;
     constexpr int CPRE = WTN / 4;          // 4-column chunks per staged row
     constexpr int RPIT = 64 / CPRE;        // rows per read iteration
+    // The requantizing store is long; unrolling its row loop fully would make
+    // the block loop too large to unroll, and the accumulator array would then
+    // be indexed at run time (scratch memory).
+    constexpr int IT_UNROLL = (E == EpiKind::Q8) ? 4 : 32 / RPIT;
+    // Requantization channels of this lane's 4 columns (fixed for the whole
+    // tile when they are columns).
+    float col_s[4] = {0, 0, 0, 0};
+    int32_t col_b[4] = {0, 0, 0, 0};
+    if constexpr (E == EpiKind::Q8) {
+        if (ep.axis) {
+            const int ci = wn * WTN + (lane % CPRE) * 4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                col_s[e] = q_scale[ci + e];
+                col_b[e] = q_bias[ci + e];
+            }
+        }
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -377,7 +425,7 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
         __builtin_amdgcn_wave_barrier();
         const int grow0 = m0 + wm * WTM + i * 32;
         const int gcol0 = n0 + wn * WTN;
-#pragma unroll
+#pragma unroll IT_UNROLL
         for (int it = 0; it < 32 / RPIT; ++it) {
             const int row = it * RPIT + lane / CPRE;
             const int c4 = (lane % CPRE) * 4;
@@ -385,8 +433,20 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
             v4_t v4 = *(const v4_t *)(stg + row * EPI_LD + c4);
             val_t v[4] = {v4[0], v4[1], v4[2], v4[3]};
             const int grow = grow0 + row;
+            float s4[4] = {col_s[0], col_s[1], col_s[2], col_s[3]};
+            int32_t b4[4] = {col_b[0], col_b[1], col_b[2], col_b[3]};
+            if constexpr (E == EpiKind::Q8) {
+                if (!ep.axis) {
+                    const int ri = grow - q_ch0 < BM ? grow - q_ch0 : BM - 1;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        s4[e] = q_scale[ri];
+                        b4[e] = q_bias[ri];
+                    }
+                }
+            }
             if (grow < args.M && gcol0 + c4 < args.N)
-                store4<E, val_t>(ep, z, grow, gcol0 + c4, args.N, v);
+                store4<E, val_t>(ep, z, grow, gcol0 + c4, args.N, v, s4, b4);
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_wave_barrier();
