@@ -332,23 +332,33 @@ bool skinny_enabled() {
 }
 
 // Tile choice: the tile with the smallest makespan.  Tiles spread evenly over
-// the CUs, so the busiest CU runs ceil(tiles / CUs) of them, up to `occ` at a
-// time; a CU running n tiles of BM x BN together delivers eff[n-1] of its
-// matrix-core peak.  The efficiencies are measured cycles per K stage of
-// each tile against its MFMA-bound cycles (4096^3 and 2048 x 11008 x 4096
-// int8 runs); small tiles lose most to load issue and the stage barrier.
-Tile pick_tile(int64_t M, int64_t N, int64_t batch) {
+// the CUs, so the busiest CU runs per_cu = ceil(tiles / CUs) of them, up to
+// `occ` at a time.  A tile costs its main loop, BM*BN*kf / eff[n-1] (kf: K
+// bytes per row relative to 4096; n tiles sharing a CU deliver eff[n-1] of
+// its matrix-core peak), plus its epilogue, BM*BN*c_epi, of which a fraction
+// `hide` overlaps the next tile's main loop when the CU has more than one
+// (a second workgroup, or a second wave per SIMD, keeps the matrix cores busy
+// meanwhile); the last epilogue is never hidden.  Every tile also waits once
+// for its first stages to arrive (kTileLatency, ~2 us).  Calibrated on
+// measured int8 runs (4096^3; 2048 x 11008 x 4096 with i32 and requantized
+// output) and checked against bf16 batched 64 x 512 x 512 x 128 and small
+// f32/int8 squares.
+Tile pick_tile(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind kind) {
     bool forced;
     Tile t = env_tile(&forced);
     if (forced) return t;
-    struct Cand { Tile t; int bm, bn, occ; double eff[2]; };
+    struct Cand { Tile t; int bm, bn, occ; double eff[2], hide; };
     static const Cand cands[] = {
-        {Tile::T256x256, 256, 256, 1, {0.83, 0.83}},
-        {Tile::T256x128o2, 256, 128, 2, {0.45, 0.60}},
-        {Tile::T256x128, 256, 128, 1, {0.55, 0.55}},
-        {Tile::T128x128, 128, 128, 2, {0.35, 0.50}},
-        {Tile::T64x64, 64, 64, 2, {0.20, 0.30}},
+        {Tile::T256x256, 256, 256, 1, {0.83, 0.83}, 0.0},
+        {Tile::T256x256w8, 256, 256, 1, {0.81, 0.81}, 0.6},
+        {Tile::T256x128o2, 256, 128, 2, {0.45, 0.60}, 0.5},
+        {Tile::T256x128, 256, 128, 1, {0.55, 0.55}, 0.0},
+        {Tile::T128x128, 128, 128, 2, {0.35, 0.50}, 0.5},
+        {Tile::T64x64, 64, 64, 2, {0.20, 0.30}, 0.5},
     };
+    const double c_epi = kind == EpiKind::Q8 ? 0.97 : (kind == EpiKind::BF16 ? 0.2 : 0.28);
+    constexpr double kTileLatency = 4000.0;  // in the units of area / eff
+    const double kf = (double)std::max<int64_t>(kbytes, 64) / 4096.0;
     double best = 1e300;
     Tile bt = Tile::T64x64;
     const int64_t cus = g_num_cus > 0 ? g_num_cus : 256;
@@ -356,7 +366,10 @@ Tile pick_tile(int64_t M, int64_t N, int64_t batch) {
         const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * batch;
         const int64_t per_cu = (tiles + cus - 1) / cus;
         const int together = (int)std::min<int64_t>(per_cu, c.occ);
-        const double cost = (double)per_cu * c.bm * c.bn / c.eff[together - 1];
+        const double area = (double)c.bm * c.bn;
+        const double exposed = per_cu - c.hide * (per_cu - 1);
+        const double cost = per_cu * area * kf / c.eff[together - 1] +
+                            (area * c_epi + kTileLatency) * exposed;
         if (cost < best * 0.999) { best = cost; bt = c.t; }
     }
     return bt;
@@ -472,7 +485,7 @@ int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t
     args.N = (int32_t)N;
     args.K = (int32_t)k;
     args.batch = (int32_t)batch;
-    e = launch_mma(in, pick_tile(M, N, batch), args, ep, tl_stream);
+    e = launch_mma(in, pick_tile(M, N, batch, k * (int64_t)esz, ep.kind), args, ep, tl_stream);
     if (e != hipSuccess) return hip_fail(e, "mfma launch");
     return finish("mfma gemm");
 }
