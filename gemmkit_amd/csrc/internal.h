@@ -63,6 +63,8 @@ enum class Tile : int {
     T256x128o2 = 5,  // 3-stage ring: two workgroups per CU
 };
 
+hipError_t launch_mma_i8(Tile tile, const MmaArgs &args, const EpiParams &ep, hipStream_t stream);
+hipError_t launch_mma_bf16(Tile tile, const MmaArgs &args, const EpiParams &ep, hipStream_t stream);
 hipError_t launch_mma(InType in, Tile tile, const MmaArgs &args, const EpiParams &ep,
                       hipStream_t stream);
 

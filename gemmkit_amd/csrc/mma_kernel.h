@@ -1,5 +1,7 @@
-// mfma_gemm.hip -- LDS-tiled CDNA4 matrix-core GEMM for i8 -> i32, bf16 -> f32 and
-// f32 -> f32, with the epilogue applied to the accumulator registers.
+#pragma once
+// mma_kernel.h -- LDS-tiled CDNA4 matrix-core GEMM for i8 -> i32, bf16 -> f32 and
+// f32 -> f32, with the epilogue applied to the accumulator registers.  The
+// template is instantiated per input type in mfma_{i8,bf16,f32}.hip.
 //
 // Replaces gemmkit's packing + BLIS 5-loop + microkernel layers
 // (src/driver.rs:402-944, src/kernel/int.rs:138-490, src/kernel/mixed.rs:31-400,
@@ -189,7 +191,7 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     constexpr int RPI = 1024 / BK;        // stage rows one instruction fills
     constexpr int CPR = BK / 16;          // 16-byte chunks per stage row
     constexpr int SUB = BK / 32;          // MFMA sub-steps per stage
-    constexpr int EPI_LD = WTN + 8;       // staged-epilogue row stride (4-byte words)
+    constexpr int EPI_LD = WTN + 4;       // staged-epilogue row stride (4-byte words)
     constexpr int SMEM = NS * STAGE;
     static_assert(NI % NWAVES == 0 && TM >= 1 && TN >= 1, "tile too small");
     static_assert(NWAVES * 32 * EPI_LD * 4 <= SMEM, "epilogue staging does not fit");
@@ -290,7 +292,7 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int j = 0; j < TN; ++j) acc[i][j] = M::step(af[set][i], bf[set][j], acc[i][j]);
+            for (int j = 0; j < TN; ++j) acc[i][j] = M::step(bf[set][j], af[set][i], acc[i][j]);
     };
 
     // Every iteration issues exactly one stage of loads: past the end of K they
@@ -387,9 +389,17 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
         }
     }
 
-    // Staged epilogue.  Wave region: 32 rows x EPI_LD words.  Written from the
-    // MFMA layout (register r of lane l: row 8*(r/4) + 4*(l/32) + r%4, column
-    // l%32 of block j), read back as 4-column chunks, one row per CPRE lanes.
+    // Staged epilogue.  The MFMAs take B^T's fragment as their first operand,
+    // so a 32x32 accumulator block holds C^T: register 4g+e of lane l is C row
+    // l%32, column 8g + 4*(l/32) + e, i.e. four consecutive columns per lane
+    // and group.  Each 32-row block goes to LDS as 16-byte writes (the ring is
+    // free now; 32 rows x EPI_LD words per wave, EPI_LD = 4 mod 64 words so the
+    // writes and the row reads below are conflict-free) and comes back as rows:
+    // one row per CPRE lanes, whole 16-byte chunks, so the global stores write
+    // full contiguous rows (storing the registers directly would write 32-byte
+    // pieces of 32 rows per instruction, which the memory system handles at a
+    // fraction of the rate).  The barrier also retires the zero-fill loads past
+    // the end of K.
     __syncthreads();
     val_t *stg = (val_t *)smem + wave * 32 * EPI_LD;
     constexpr int CPRE = WTN / 4;          // 4-column chunks per staged row
@@ -414,12 +424,14 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
+        typedef val_t v4_t __attribute__((ext_vector_type(4)));
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = (r >> 2) * 8 + lhalf * 4 + (r & 3);
-                stg[row * EPI_LD + j * 32 + lrow] = (val_t)acc[i][j][r];
+            for (int g = 0; g < 4; ++g) {
+                const v4_t w = {(val_t)acc[i][j][4 * g], (val_t)acc[i][j][4 * g + 1],
+                                (val_t)acc[i][j][4 * g + 2], (val_t)acc[i][j][4 * g + 3]};
+                *(v4_t *)(stg + lrow * EPI_LD + j * 32 + 8 * g + 4 * lhalf) = w;
             }
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes done
         __builtin_amdgcn_wave_barrier();
@@ -429,7 +441,6 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
         for (int it = 0; it < 32 / RPIT; ++it) {
             const int row = it * RPIT + lane / CPRE;
             const int c4 = (lane % CPRE) * 4;
-            typedef val_t v4_t __attribute__((ext_vector_type(4)));
             v4_t v4 = *(const v4_t *)(stg + row * EPI_LD + c4);
             val_t v[4] = {v4[0], v4[1], v4[2], v4[3]};
             const int grow = grow0 + row;
@@ -453,7 +464,7 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     }
 }
 
-template <InType T, EpiKind E, int BM, int BN, int WM, int WN, int NS = 4>
+template <InType T, EpiKind E, int BM, int BN, int WM, int WN, int NS>
 static hipError_t launch_one(const MmaArgs &args, const EpiParams &ep, hipStream_t stream) {
     int tiles = ((args.M + BM - 1) / BM) * ((args.N + BN - 1) / BN);
     dim3 grid(tiles, 1, args.batch);
@@ -466,30 +477,12 @@ template <InType T, EpiKind E>
 static hipError_t launch_tile(Tile tile, const MmaArgs &args, const EpiParams &ep,
                               hipStream_t stream) {
     switch (tile) {
-    case Tile::T256x256: return launch_one<T, E, 256, 256, 2, 2>(args, ep, stream);
-    case Tile::T256x256w8: return launch_one<T, E, 256, 256, 2, 4>(args, ep, stream);
-    case Tile::T256x128: return launch_one<T, E, 256, 128, 2, 2>(args, ep, stream);
+    case Tile::T256x256: return launch_one<T, E, 256, 256, 2, 2, 4>(args, ep, stream);
+    case Tile::T256x256w8: return launch_one<T, E, 256, 256, 2, 4, 4>(args, ep, stream);
+    case Tile::T256x128: return launch_one<T, E, 256, 128, 2, 2, 4>(args, ep, stream);
     case Tile::T256x128o2: return launch_one<T, E, 256, 128, 2, 2, 3>(args, ep, stream);
-    case Tile::T128x128: return launch_one<T, E, 128, 128, 2, 2>(args, ep, stream);
-    case Tile::T64x64: return launch_one<T, E, 64, 64, 2, 2>(args, ep, stream);
-    }
-    return hipErrorInvalidValue;
-}
-
-hipError_t launch_mma(InType in, Tile tile, const MmaArgs &args, const EpiParams &ep,
-                      hipStream_t stream) {
-    switch (in) {
-    case InType::I8:
-        if (ep.kind == EpiKind::I32) return launch_tile<InType::I8, EpiKind::I32>(tile, args, ep, stream);
-        if (ep.kind == EpiKind::Q8) return launch_tile<InType::I8, EpiKind::Q8>(tile, args, ep, stream);
-        break;
-    case InType::BF16:
-        if (ep.kind == EpiKind::F32) return launch_tile<InType::BF16, EpiKind::F32>(tile, args, ep, stream);
-        if (ep.kind == EpiKind::BF16) return launch_tile<InType::BF16, EpiKind::BF16>(tile, args, ep, stream);
-        break;
-    case InType::F32:
-        if (ep.kind == EpiKind::F32) return launch_tile<InType::F32, EpiKind::F32>(tile, args, ep, stream);
-        break;
+    case Tile::T128x128: return launch_one<T, E, 128, 128, 2, 2, 4>(args, ep, stream);
+    case Tile::T64x64: return launch_one<T, E, 64, 64, 2, 2, 4>(args, ep, stream);
     }
     return hipErrorInvalidValue;
 }
