@@ -15,7 +15,8 @@ int8 linear layer with a prepacked weight (2048 x 4096 x 11008, 16 calls per
 step), batched bf16 attention scores (64 x 512 x 512 x 128, f32 out), bf16
 4096^3 (the matrix-core-bound bf16 shape), int8 GEMV (W 14336 x 4096, M = 1
 and 8; five weight copies rotate so the 256 MB Infinity Cache cannot serve
-them), f32 GEMV 16384^2, and the f32 512^3 case.
+them), f32 GEMV 16384^2, the f32 512^3 case, bf16 4096^3 with a fused bias
+and ReLU, and prepacked weights at small batch (k = n = 2048, m = 8 and 64).
 
 roofline: algorithmic ops of one 4096^3 launch (2*4096^3) over the average
 launch time from the HIP events, against MI355X's published dense int8 peak
@@ -277,6 +278,57 @@ def run_extras(args, workloads, want, timed, dev, gk, np, torch):
         call = lambda: gk.gemm_unchecked(n, n, n, 1.0, a, n, 1, b, n, 1, 0.0, c, n, 1)  # noqa: E731
         ms = timed(call, steps, warm)
         workloads["f32_gemm_512"] = {"ms": ms, "TFLOPS": 2 * n ** 3 / ms / 1e9}
+
+    # bf16 4096^3 with bf16 output: plain, and fused with a per-column bias and
+    # ReLU (the epilogue's cost is the difference)
+    if want("bf16_fused_4096"):
+        n = 4096
+        a = torch.randn(n * n, generator=g).to(torch.bfloat16).to(dev)
+        b = torch.randn(n * n, generator=g).to(torch.bfloat16).to(dev)
+        c = torch.empty(n * n, dtype=torch.bfloat16, device=dev)
+        bias = torch.randn(n, generator=g).to(torch.bfloat16).to(dev)
+        A, B = gk.MatRef.from_row_major(a, n, n), gk.MatRef(b, n, n, 1, n)
+        C = gk.MatMut.from_row_major(c, n, n)
+        plain = timed(lambda: gk.gemm(1.0, A, B, 0.0, C), steps, warm)
+        fused = timed(lambda: gk.gemm_fused(1.0, A, B, 0.0, C, gk.Bias.PerCol(bias),
+                                            gk.Activation.Relu), steps, warm)
+        workloads["bf16_fused_4096"] = {"ms_plain": plain, "ms_fused": fused,
+                                        "TFLOPS_fused": 2 * n ** 3 / fused / 1e9,
+                                        "frac_bf16_peak": 2 * n ** 3 / (fused * 1e-3) / 2.5e15}
+        del a, b, c
+
+    # prepacked weight at small batch (k = n = 2048, m = 8 and 64; A and C
+    # column-major, f32 B row-major and i8 B column-major before packing), as
+    # gemmkit's fixed-weight inference benchmark
+    if want("packed_small_m"):
+        k = n = 2048
+        bf = torch.randn(k * n, generator=g).to(dev)
+        pf = gk.prepack_rhs(gk.MatRef.from_row_major(bf, k, n))
+        bi = i8(k * n)
+        pi = gk.prepack_rhs_i8(gk.MatRef.from_col_major(bi, k, n))
+        res = {}
+        for m in (8, 64):
+            af = torch.randn(m * k, generator=g).to(dev)
+            cf = torch.empty(m * n, device=dev)
+            ai = i8(m * k)
+            ci = torch.empty(m * n, dtype=torch.int32, device=dev)
+            t = {
+                "f32_plain": lambda: gk.gemm(1.0, gk.MatRef.from_col_major(af, m, k),
+                                             gk.MatRef.from_row_major(bf, k, n), 0.0,
+                                             gk.MatMut.from_col_major(cf, m, n)),
+                "f32_packed_b": lambda: gk.gemm_packed_b(1.0, gk.MatRef.from_col_major(af, m, k),
+                                                         pf, 0.0, gk.MatMut.from_col_major(cf, m, n)),
+                "i8_plain": lambda: gk.gemm_i8(1, gk.MatRef.from_col_major(ai, m, k),
+                                               gk.MatRef.from_col_major(bi, k, n), 0,
+                                               gk.MatMut.from_col_major(ci, m, n)),
+                "i8_packed_b": lambda: gk.gemm_i8_packed_b(1, gk.MatRef.from_col_major(ai, m, k),
+                                                           pi, 0, gk.MatMut.from_col_major(ci, m, n)),
+            }
+            for name, fn in t.items():
+                ms = timed(fn, steps, warm)
+                res[f"{name}_m{m}"] = {"us": ms * 1e3, "GFLOPS": 2 * m * n * k / ms / 1e6}
+        workloads["packed_small_m"] = res
+        del bf, pf, bi, pi
 
     # a plain elementwise kernel over 1 GiB in, 1 GiB out (reads and writes
     # each byte once): the calibration workload for the HBM byte counters

@@ -19,6 +19,15 @@ reference (gemmkit/src/...)      here
 ``prepack_rhs_i8``               :func:`prepack_rhs_i8` -> :class:`PackedRhs`
 ``gemm_i8_packed_b(_with)``      :func:`gemm_i8_packed_b`
 ``gemm_batched(_with)``          :func:`gemm_batched`
+``prepack_rhs`` (f32, bf16)      :func:`prepack_rhs` -> :class:`PackedRhs`
+``gemm_packed_b(_with)``         :func:`gemm_packed_b`, :func:`gemm_packed_b_unchecked`
+``Bias`` / ``Activation``        :class:`Bias` / :class:`Activation`
+  (api/fused.rs:17-31)
+``gemm_fused(_with)``            :func:`gemm_fused`, :func:`gemm_fused_unchecked`
+``gemm_batched_fused(_with)``    :func:`gemm_batched_fused`,
+                                 :func:`gemm_batched_fused_unchecked`
+``gemm_packed_b_fused(_with)``   :func:`gemm_packed_b_fused`,
+                                 :func:`gemm_packed_b_fused_unchecked`
 ``Parallelism``                  :class:`Parallelism` (accepted, ignored: the
                                  device grid decides)
 ``Workspace``                    :class:`Workspace` (a device scratch arena)
@@ -45,7 +54,7 @@ from typing import Optional, Sequence, Union
 import torch
 
 from . import _lib
-from ._lib import MatMutC, MatRefC, RequantizeC
+from ._lib import BiasC, MatMutC, MatRefC, RequantizeC
 
 __all__ = [
     "GemmkitError", "MatRef", "MatMut", "Parallelism", "Workspace", "RequantScale",
@@ -54,7 +63,10 @@ __all__ = [
     "gemm_i8_requant_u8_unchecked", "prepack_rhs_i8", "gemm_i8_packed_b",
     "gemm_i8_packed_b_unchecked", "gemm_i8_packed_b_requant", "gemm_i8_packed_b_requant_u8",
     "gemm_i8_packed_b_requant_unchecked",
-    "gemm_batched", "gemm_batched_unchecked", "gemm_batched_bf16_f32out", "set_synchronous",
+    "gemm_batched", "gemm_batched_unchecked", "gemm_batched_bf16_f32out", "prepack_rhs",
+    "gemm_packed_b", "gemm_packed_b_unchecked", "Bias", "Activation", "gemm_fused",
+    "gemm_fused_unchecked", "gemm_batched_fused", "gemm_batched_fused_unchecked",
+    "gemm_packed_b_fused", "gemm_packed_b_fused_unchecked", "set_synchronous",
     "library_path", "version",
 ]
 
@@ -366,7 +378,8 @@ def gemm_i8_requant_u8_unchecked(m, k, n, a, rsa, csa, b, rsb, csb, scale, row_s
 # ---------------------------------------------------------------- prepacked B
 
 class PackedRhs:
-    """PackedRhs<i8> (src/api/packed.rs:34-52): B packed once on the device."""
+    """PackedRhs<T> (src/api/packed.rs:34-52): B packed once on the device
+    (i8 from :func:`prepack_rhs_i8`, f32/bf16 from :func:`prepack_rhs`)."""
 
     def __init__(self, handle):
         self._h = handle
@@ -496,3 +509,233 @@ def gemm_batched_bf16_f32out(batch: int, alpha: float, a: MatRef, a_batch_stride
         _ws(ws), batch, float(alpha), a._c(torch.bfloat16, "A"), a_batch_stride,
         b._c(torch.bfloat16, "B"), b_batch_stride, float(beta), c._c(torch.float32, "C"),
         c_batch_stride, _par(par)))
+
+
+# ------------------------------------------------------ prepacked f32 / bf16 B
+
+def prepack_rhs(b: MatRef) -> PackedRhs:
+    """``prepack_rhs::<f32|bf16>`` (src/api/packed.rs:67-170)."""
+    _bind_stream()
+    L = _lib.lib()
+    out = C.c_void_p()
+    dt = b.data.dtype
+    if dt == torch.float32:
+        _check(L.gk_prepack_rhs_f32(b._c(dt, "B"), C.byref(out)))
+    elif dt == torch.bfloat16:
+        _check(L.gk_prepack_rhs_bf16(b._c(dt, "B"), C.byref(out)))
+    else:
+        raise TypeError(f"gemmkit_amd: prepack_rhs supports float32 and bfloat16, got {dt}")
+    return PackedRhs(out.value)
+
+
+def gemm_packed_b(alpha, a: MatRef, packed: PackedRhs, beta, c: MatMut,
+                  par: Optional[Parallelism] = None, ws: Optional[Workspace] = None) -> None:
+    """``gemm_packed_b(_with)`` (src/api/packed.rs:175-260): column-major-ish C."""
+    _bind_stream()
+    L = _lib.lib()
+    dt = a.data.dtype
+    if dt == torch.float32:
+        _check(L.gk_gemm_packed_b_f32(_ws(ws), float(alpha), a._c(dt, "A"), packed.handle,
+                                      float(beta), c._c(dt, "C"), _par(par)))
+    elif dt == torch.bfloat16:
+        _check(L.gk_gemm_packed_b_bf16(_ws(ws), _bf16_bits(alpha), a._c(dt, "A"), packed.handle,
+                                       _bf16_bits(beta), c._c(dt, "C"), _par(par)))
+    else:
+        raise TypeError(f"gemmkit_amd: gemm_packed_b supports float32 and bfloat16, got {dt}")
+
+
+def gemm_packed_b_unchecked(alpha, m, a, rsa, csa, packed: PackedRhs, beta, c, rsc, csc,
+                            par=None, ws=None, a_off=0, c_off=0) -> None:
+    """``gemm_packed_b_unchecked(_with)`` (src/api/packed.rs:270-365)."""
+    _bind_stream()
+    L = _lib.lib()
+    if a.dtype == torch.float32:
+        _check(L.gk_gemm_packed_b_f32_unchecked(_ws(ws), float(alpha), m, _ptr(a, a_off), rsa, csa,
+                                                packed.handle, float(beta), _ptr(c, c_off), rsc,
+                                                csc, _par(par)))
+    elif a.dtype == torch.bfloat16:
+        _check(L.gk_gemm_packed_b_bf16_unchecked(_ws(ws), _bf16_bits(alpha), m, _ptr(a, a_off),
+                                                 rsa, csa, packed.handle, _bf16_bits(beta),
+                                                 _ptr(c, c_off), rsc, csc, _par(par)))
+    else:
+        raise TypeError("gemmkit_amd: gemm_packed_b_unchecked supports float32 and bfloat16")
+
+
+# ------------------------------------------------------ fused bias/activation
+
+BIAS_PER_ROW = 0
+BIAS_PER_COL = 1
+
+
+class Bias:
+    """Bias (src/api/fused.rs:17-23): ``PerRow(tensor)`` (length m) or
+    ``PerCol(tensor)`` (length n), of the GEMM's element type."""
+
+    def __init__(self, dim: int, data: torch.Tensor):
+        self.dim, self.data = dim, data
+
+    @staticmethod
+    def PerRow(data: torch.Tensor) -> "Bias":  # noqa: N802 -- mirrors the Rust variant
+        return Bias(BIAS_PER_ROW, data)
+
+    @staticmethod
+    def PerCol(data: torch.Tensor) -> "Bias":  # noqa: N802
+        return Bias(BIAS_PER_COL, data)
+
+    def _c(self, dtype: torch.dtype) -> BiasC:
+        d = _slice(self.data, "bias")
+        if d.dtype != dtype:
+            raise TypeError(f"gemmkit_amd: bias must be {dtype}, got {d.dtype}")
+        return BiasC(d.data_ptr(), d.numel(), self.dim)
+
+
+class Activation:
+    """Activation (src/api/fused.rs:25-31): ``Relu`` or ``LeakyRelu(slope)``."""
+
+    def __init__(self, kind: int, slope: float = 0.0):
+        self.kind, self.slope = kind, float(slope)
+
+    @staticmethod
+    def LeakyRelu(slope: float) -> "Activation":  # noqa: N802
+        return Activation(2, slope)
+
+
+Activation.Relu = Activation(1)  # type: ignore[attr-defined]
+
+
+def _fused_args(dt: torch.dtype, bias: Optional[Bias], act: Optional[Activation]):
+    """(gk_bias pointer or None, act code, slope in the ABI's scalar type)."""
+    bc = None if bias is None else C.byref(bias._c(dt))
+    kind = 0 if act is None else act.kind
+    slope = 0.0 if act is None else act.slope
+    return bc, kind, (_bf16_bits(slope) if dt == torch.bfloat16 else slope)
+
+
+def _raw_bias(bias: Optional[torch.Tensor], dim: int):
+    return _ptr(bias), int(dim), (1 if bias is not None else 0)
+
+
+def gemm_fused(alpha, a: MatRef, b: MatRef, beta, c: MatMut, bias: Optional[Bias] = None,
+               act: Optional[Activation] = None, par: Optional[Parallelism] = None,
+               ws: Optional[Workspace] = None) -> None:
+    """``gemm_fused(_with)`` (src/api/fused.rs:61-140):
+    C <- act(alpha*A*B + beta*C + bias), float32 or bfloat16."""
+    _bind_stream()
+    L = _lib.lib()
+    dt = a.data.dtype
+    bc, kind, slope = _fused_args(dt, bias, act)
+    if dt == torch.float32:
+        _check(L.gk_gemm_fused_f32(_ws(ws), float(alpha), a._c(dt, "A"), b._c(dt, "B"),
+                                   float(beta), c._c(dt, "C"), bc, kind, slope, _par(par)))
+    elif dt == torch.bfloat16:
+        _check(L.gk_gemm_fused_bf16(_ws(ws), _bf16_bits(alpha), a._c(dt, "A"), b._c(dt, "B"),
+                                    _bf16_bits(beta), c._c(dt, "C"), bc, kind, slope, _par(par)))
+    else:
+        raise TypeError(f"gemmkit_amd: gemm_fused supports float32 and bfloat16, got {dt}")
+
+
+def gemm_fused_unchecked(m, k, n, alpha, a, rsa, csa, b, rsb, csb, beta, c, rsc, csc,
+                         bias=None, bias_dim=BIAS_PER_ROW, act: Optional[Activation] = None,
+                         par=None, ws=None, a_off=0, b_off=0, c_off=0) -> None:
+    """``gemm_fused_unchecked(_with)`` (src/api/fused.rs:149-230)."""
+    _bind_stream()
+    L = _lib.lib()
+    bp, bd, hb = _raw_bias(bias, bias_dim)
+    _, kind, slope = _fused_args(a.dtype, None, act)
+    if a.dtype == torch.float32:
+        _check(L.gk_gemm_fused_f32_unchecked(_ws(ws), m, k, n, float(alpha), _ptr(a, a_off), rsa,
+                                             csa, _ptr(b, b_off), rsb, csb, float(beta),
+                                             _ptr(c, c_off), rsc, csc, bp, bd, hb, kind, slope,
+                                             _par(par)))
+    elif a.dtype == torch.bfloat16:
+        _check(L.gk_gemm_fused_bf16_unchecked(_ws(ws), m, k, n, _bf16_bits(alpha), _ptr(a, a_off),
+                                              rsa, csa, _ptr(b, b_off), rsb, csb,
+                                              _bf16_bits(beta), _ptr(c, c_off), rsc, csc, bp, bd,
+                                              hb, kind, slope, _par(par)))
+    else:
+        raise TypeError("gemmkit_amd: gemm_fused_unchecked supports float32 and bfloat16")
+
+
+def gemm_batched_fused(batch: int, alpha, a: MatRef, a_batch_stride: int, b: MatRef,
+                       b_batch_stride: int, beta, c: MatMut, c_batch_stride: int,
+                       bias: Optional[Bias] = None, act: Optional[Activation] = None,
+                       par: Optional[Parallelism] = None, ws: Optional[Workspace] = None) -> None:
+    """``gemm_batched_fused(_with)`` (src/api/batched.rs:307-450): one shared bias."""
+    _bind_stream()
+    L = _lib.lib()
+    dt = a.data.dtype
+    bc, kind, slope = _fused_args(dt, bias, act)
+    if dt == torch.float32:
+        _check(L.gk_gemm_batched_fused_f32(_ws(ws), batch, float(alpha), a._c(dt, "A"),
+                                           a_batch_stride, b._c(dt, "B"), b_batch_stride,
+                                           float(beta), c._c(dt, "C"), c_batch_stride, bc, kind,
+                                           slope, _par(par)))
+    elif dt == torch.bfloat16:
+        _check(L.gk_gemm_batched_fused_bf16(_ws(ws), batch, _bf16_bits(alpha), a._c(dt, "A"),
+                                            a_batch_stride, b._c(dt, "B"), b_batch_stride,
+                                            _bf16_bits(beta), c._c(dt, "C"), c_batch_stride, bc,
+                                            kind, slope, _par(par)))
+    else:
+        raise TypeError(f"gemmkit_amd: gemm_batched_fused supports float32 and bfloat16, got {dt}")
+
+
+def gemm_batched_fused_unchecked(batch, m, k, n, alpha, a, rsa, csa, a_bs, b, rsb, csb, b_bs,
+                                 beta, c, rsc, csc, c_bs, bias=None, bias_dim=BIAS_PER_ROW,
+                                 act: Optional[Activation] = None, par=None, ws=None) -> None:
+    """``gemm_batched_fused_unchecked(_with)`` (src/api/batched.rs:459-590)."""
+    _bind_stream()
+    L = _lib.lib()
+    bp, bd, hb = _raw_bias(bias, bias_dim)
+    _, kind, slope = _fused_args(a.dtype, None, act)
+    if a.dtype == torch.float32:
+        _check(L.gk_gemm_batched_fused_f32_unchecked(
+            _ws(ws), batch, m, k, n, float(alpha), _ptr(a), rsa, csa, a_bs, _ptr(b), rsb, csb,
+            b_bs, float(beta), _ptr(c), rsc, csc, c_bs, bp, bd, hb, kind, slope, _par(par)))
+    elif a.dtype == torch.bfloat16:
+        _check(L.gk_gemm_batched_fused_bf16_unchecked(
+            _ws(ws), batch, m, k, n, _bf16_bits(alpha), _ptr(a), rsa, csa, a_bs, _ptr(b), rsb,
+            csb, b_bs, _bf16_bits(beta), _ptr(c), rsc, csc, c_bs, bp, bd, hb, kind, slope,
+            _par(par)))
+    else:
+        raise TypeError("gemmkit_amd: gemm_batched_fused_unchecked supports float32 and bfloat16")
+
+
+def gemm_packed_b_fused(alpha, a: MatRef, packed: PackedRhs, beta, c: MatMut,
+                        bias: Optional[Bias] = None, act: Optional[Activation] = None,
+                        par: Optional[Parallelism] = None, ws: Optional[Workspace] = None) -> None:
+    """``gemm_packed_b_fused(_with)`` (src/api/packed.rs:684-790)."""
+    _bind_stream()
+    L = _lib.lib()
+    dt = a.data.dtype
+    bc, kind, slope = _fused_args(dt, bias, act)
+    if dt == torch.float32:
+        _check(L.gk_gemm_packed_b_fused_f32(_ws(ws), float(alpha), a._c(dt, "A"), packed.handle,
+                                            float(beta), c._c(dt, "C"), bc, kind, slope,
+                                            _par(par)))
+    elif dt == torch.bfloat16:
+        _check(L.gk_gemm_packed_b_fused_bf16(_ws(ws), _bf16_bits(alpha), a._c(dt, "A"),
+                                             packed.handle, _bf16_bits(beta), c._c(dt, "C"), bc,
+                                             kind, slope, _par(par)))
+    else:
+        raise TypeError(f"gemmkit_amd: gemm_packed_b_fused supports float32 and bfloat16, got {dt}")
+
+
+def gemm_packed_b_fused_unchecked(alpha, m, a, rsa, csa, packed: PackedRhs, beta, c, rsc, csc,
+                                  bias=None, bias_dim=BIAS_PER_ROW,
+                                  act: Optional[Activation] = None, par=None, ws=None,
+                                  a_off=0, c_off=0) -> None:
+    """``gemm_packed_b_fused_unchecked(_with)`` (src/api/packed.rs:801-950)."""
+    _bind_stream()
+    L = _lib.lib()
+    bp, bd, hb = _raw_bias(bias, bias_dim)
+    _, kind, slope = _fused_args(a.dtype, None, act)
+    if a.dtype == torch.float32:
+        _check(L.gk_gemm_packed_b_fused_f32_unchecked(
+            _ws(ws), float(alpha), m, _ptr(a, a_off), rsa, csa, packed.handle, float(beta),
+            _ptr(c, c_off), rsc, csc, bp, bd, hb, kind, slope, _par(par)))
+    elif a.dtype == torch.bfloat16:
+        _check(L.gk_gemm_packed_b_fused_bf16_unchecked(
+            _ws(ws), _bf16_bits(alpha), m, _ptr(a, a_off), rsa, csa, packed.handle,
+            _bf16_bits(beta), _ptr(c, c_off), rsc, csc, bp, bd, hb, kind, slope, _par(par)))
+    else:
+        raise TypeError("gemmkit_amd: gemm_packed_b_fused_unchecked supports float32 and bfloat16")

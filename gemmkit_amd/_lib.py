@@ -41,9 +41,15 @@ class RequantizeC(C.Structure):
                 ("axis", _i32), ("act", _i32)]
 
 
+class BiasC(C.Structure):
+    """``gk_bias``: Bias::PerRow / PerCol (src/api/fused.rs:17-23) with its length."""
+    _fields_ = [("data", _vp), ("len", _size), ("dim", _i32)]
+
+
 _REF = C.POINTER(MatRefC)
 _MUT = C.POINTER(MatMutC)
 _REQ = C.POINTER(RequantizeC)
+_BIAS = C.POINTER(BiasC)
 
 # name -> (restype, argtypes); one line per symbol of include/gemmkit_hip.h
 SIGNATURES: dict[str, tuple] = {
@@ -109,6 +115,49 @@ SIGNATURES: dict[str, tuple] = {
                                                         _vp, _sdiff, _sdiff, _sdiff, _vp, _sdiff,
                                                         _sdiff, _sdiff, _f32, _vp, _sdiff, _sdiff,
                                                         _sdiff, _u32]),
+    "gk_prepack_rhs_f32": (C.c_int, [_REF, C.POINTER(_vp)]),
+    "gk_prepack_rhs_f32_unchecked": (C.c_int, [_vp, _sdiff, _sdiff, _size, _size,
+                                               C.POINTER(_vp)]),
+    "gk_prepack_rhs_bf16": (C.c_int, [_REF, C.POINTER(_vp)]),
+    "gk_prepack_rhs_bf16_unchecked": (C.c_int, [_vp, _sdiff, _sdiff, _size, _size,
+                                                C.POINTER(_vp)]),
+    "gk_gemm_packed_b_f32": (C.c_int, [_vp, _f32, _REF, _vp, _f32, _MUT, _u32]),
+    "gk_gemm_packed_b_f32_unchecked": (C.c_int, [_vp, _f32, _size, _vp, _sdiff, _sdiff, _vp,
+                                                 _f32, _vp, _sdiff, _sdiff, _u32]),
+    "gk_gemm_packed_b_bf16": (C.c_int, [_vp, _u16, _REF, _vp, _u16, _MUT, _u32]),
+    "gk_gemm_packed_b_bf16_unchecked": (C.c_int, [_vp, _u16, _size, _vp, _sdiff, _sdiff, _vp,
+                                                  _u16, _vp, _sdiff, _sdiff, _u32]),
+    "gk_gemm_fused_f32": (C.c_int, [_vp, _f32, _REF, _REF, _f32, _MUT, _BIAS, _i32, _f32, _u32]),
+    "gk_gemm_fused_bf16": (C.c_int, [_vp, _u16, _REF, _REF, _u16, _MUT, _BIAS, _i32, _u16,
+                                     _u32]),
+    "gk_gemm_fused_f32_unchecked": (C.c_int, [_vp, _size, _size, _size, _f32, _vp, _sdiff,
+                                              _sdiff, _vp, _sdiff, _sdiff, _f32, _vp, _sdiff,
+                                              _sdiff, _vp, _i32, _u8, _i32, _f32, _u32]),
+    "gk_gemm_fused_bf16_unchecked": (C.c_int, [_vp, _size, _size, _size, _u16, _vp, _sdiff,
+                                               _sdiff, _vp, _sdiff, _sdiff, _u16, _vp, _sdiff,
+                                               _sdiff, _vp, _i32, _u8, _i32, _u16, _u32]),
+    "gk_gemm_batched_fused_f32": (C.c_int, [_vp, _size, _f32, _REF, _sdiff, _REF, _sdiff, _f32,
+                                            _MUT, _sdiff, _BIAS, _i32, _f32, _u32]),
+    "gk_gemm_batched_fused_bf16": (C.c_int, [_vp, _size, _u16, _REF, _sdiff, _REF, _sdiff, _u16,
+                                             _MUT, _sdiff, _BIAS, _i32, _u16, _u32]),
+    "gk_gemm_batched_fused_f32_unchecked": (C.c_int, [_vp, _size, _size, _size, _size, _f32, _vp,
+                                                      _sdiff, _sdiff, _sdiff, _vp, _sdiff, _sdiff,
+                                                      _sdiff, _f32, _vp, _sdiff, _sdiff, _sdiff,
+                                                      _vp, _i32, _u8, _i32, _f32, _u32]),
+    "gk_gemm_batched_fused_bf16_unchecked": (C.c_int, [_vp, _size, _size, _size, _size, _u16,
+                                                       _vp, _sdiff, _sdiff, _sdiff, _vp, _sdiff,
+                                                       _sdiff, _sdiff, _u16, _vp, _sdiff, _sdiff,
+                                                       _sdiff, _vp, _i32, _u8, _i32, _u16, _u32]),
+    "gk_gemm_packed_b_fused_f32": (C.c_int, [_vp, _f32, _REF, _vp, _f32, _MUT, _BIAS, _i32, _f32,
+                                             _u32]),
+    "gk_gemm_packed_b_fused_bf16": (C.c_int, [_vp, _u16, _REF, _vp, _u16, _MUT, _BIAS, _i32,
+                                              _u16, _u32]),
+    "gk_gemm_packed_b_fused_f32_unchecked": (C.c_int, [_vp, _f32, _size, _vp, _sdiff, _sdiff,
+                                                       _vp, _f32, _vp, _sdiff, _sdiff, _vp, _i32,
+                                                       _u8, _i32, _f32, _u32]),
+    "gk_gemm_packed_b_fused_bf16_unchecked": (C.c_int, [_vp, _u16, _size, _vp, _sdiff, _sdiff,
+                                                        _vp, _u16, _vp, _sdiff, _sdiff, _vp,
+                                                        _i32, _u8, _i32, _u16, _u32]),
 }
 
 _LIB: C.CDLL | None = None

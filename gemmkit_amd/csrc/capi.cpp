@@ -214,9 +214,10 @@ struct gk_workspace {
 };
 
 struct gk_packed_rhs {
-    int8_t *buf = nullptr;  // n x ld, k-contiguous rows (B transposed), zero padded
+    gk::InType in = gk::InType::I8;  // element type (PackedRhs<T>'s T)
+    void *buf = nullptr;             // n x ld, k-contiguous rows (B transposed), zero padded
     size_t k = 0, n = 0;
-    int64_t ld = 0;
+    int64_t ld = 0;                  // row stride in elements
 };
 
 namespace {
@@ -543,18 +544,59 @@ int exec_i8(gk_workspace *ws, size_t m, size_t k, size_t n, int32_t alpha, const
                        0, c, rsc, csc, 0, 1, packed);
 }
 
-// ---- float-family core (execute, src/dispatch.rs:345-358)
+// A lowered fused epilogue (to_fused_epi_raw, src/api.rs:354-380): the bias
+// pointer (f32, or bf16 for bf16 output) with its user-frame axis, and the
+// activation.
+struct FusedSpec {
+    const void *bias;
+    int32_t dim;    // GK_BIAS_PER_ROW / GK_BIAS_PER_COL
+    int32_t act;    // GK_ACT_NONE / GK_ACT_RELU / GK_ACT_LEAKY_RELU
+    float slope;
+};
+
+// The raw tier's enum arguments: values outside the reference's enums.
+int check_fused_enums(const FusedSpec &fx) {
+    if (fx.bias && fx.dim != GK_BIAS_PER_ROW && fx.dim != GK_BIAS_PER_COL)
+        return fail(GK_ERR_ARG, "gemmkit: bias dim (%d) must be 0 (PerRow) or 1 (PerCol)", fx.dim);
+    if (fx.act != GK_ACT_NONE && fx.act != GK_ACT_RELU && fx.act != GK_ACT_LEAKY_RELU)
+        return fail(GK_ERR_ARG,
+                    "gemmkit: activation (%d) must be 0 (none), 1 (Relu) or 2 (LeakyRelu)", fx.act);
+    return GK_OK;
+}
+
+// ---- float-family core (execute, src/dispatch.rs:345-358; execute_fused,
+// src/dispatch/float.rs:661-680; execute_packed(_fused), src/dispatch.rs:366-380,
+// src/dispatch/float.rs:692-735)
 int exec_float(gk_workspace *ws, InType in, EpiKind kind, size_t batch, size_t m, size_t k,
                size_t n, float alpha, const void *a, ptrdiff_t rsa, ptrdiff_t csa, ptrdiff_t bsa,
                const void *b, ptrdiff_t rsb, ptrdiff_t csb, ptrdiff_t bsb, float beta, void *c,
-               ptrdiff_t rsc, ptrdiff_t csc, ptrdiff_t bsc) {
+               ptrdiff_t rsc, ptrdiff_t csc, ptrdiff_t bsc, const FusedSpec *fx = nullptr,
+               const gk_packed_rhs *packed = nullptr) {
     int r;
     if ((r = device_init())) return r;
+    if (fx && (r = check_fused_enums(*fx))) return r;
     if (batch == 0 || m == 0 || n == 0) return ok();
     if (!dims_fit(m, k, n, batch)) return fail(GK_ERR_OVERFLOW, "gemmkit: dimensions exceed 2^31-1");
-    if (k == 0 || alpha == 0.0f) return scale_c(kind, c, m, n, rsc, csc, batch, bsc, 0, beta);
-    return run_product(ws, in, epi_float(kind, alpha, beta), m, k, n, a, rsa, csa, bsa, b, rsb,
-                       csb, bsb, c, rsc, csc, bsc, batch);
+    EpiParams ep = epi_float(kind, alpha, beta);
+    if (fx) {
+        ep.fbias = fx->bias;
+        ep.axis = fx->bias ? fx->dim : 0;
+        ep.act = fx->act;
+        ep.slope = fx->slope;
+        ep.fused = (fx->bias != nullptr || fx->act != GK_ACT_NONE) ? 1 : 0;
+    }
+    if (k == 0 || alpha == 0.0f) {
+        if (!ep.fused) return scale_c(kind, c, m, n, rsc, csc, batch, bsc, 0, beta);
+        ep.c = c;
+        ep.rsc = rsc;
+        ep.csc = csc;
+        ep.bsc = bsc;
+        hipError_t e = launch_fused_fill(ep, (int64_t)m, (int64_t)n, (int64_t)batch, tl_stream);
+        if (e != hipSuccess) return hip_fail(e, "fused fill launch");
+        return finish("fused fill");
+    }
+    return run_product(ws, in, ep, m, k, n, a, rsa, csa, bsa, b, rsb, csb, bsb, c, rsc, csc, bsc,
+                       batch, packed);
 }
 
 // ---- requant core (execute_int_requant, src/dispatch/int.rs:672-700)
@@ -744,6 +786,195 @@ int validate_batched_views(size_t batch, const gk_mat_ref *a, ptrdiff_t a_bs, co
     return GK_OK;
 }
 
+// ---- fused epilogue selectors (src/api.rs:326-380, src/adapter.rs:130-166)
+
+// Lowers the checked tier's optional bias and activation into `out`, with the
+// reference's checks: the bias length matches its axis (m for PerRow, n for
+// PerCol), the bias does not overlap C's slice, a LeakyRelu slope is finite.
+// `sb`/`so`: bias and C element sizes in bytes.
+int lower_fused(const gk_bias *bias, int32_t act, float slope, size_t m, size_t n,
+                const gk_mat_mut *c, size_t sb, size_t so, FusedSpec *out) {
+    *out = FusedSpec{nullptr, GK_BIAS_PER_ROW, act, slope};
+    if (bias) {
+        if (bias->dim == GK_BIAS_PER_ROW) {
+            if (bias->len != m)
+                return fail(GK_ERR_SHAPE, "gemmkit: PerRow bias length (%zu) != A.rows (%zu)",
+                            bias->len, m);
+        } else if (bias->dim == GK_BIAS_PER_COL) {
+            if (bias->len != n)
+                return fail(GK_ERR_SHAPE, "gemmkit: PerCol bias length (%zu) != B.cols (%zu)",
+                            bias->len, n);
+        } else {
+            return fail(GK_ERR_ARG, "gemmkit: bias dim (%d) must be 0 (PerRow) or 1 (PerCol)",
+                        bias->dim);
+        }
+        if (overlaps_bytes(c->data, c->len, so, bias->data, bias->len, sb))
+            return fail(GK_ERR_ALIAS, "gemmkit: bias slice overlaps C");
+        out->bias = bias->data;
+        out->dim = bias->dim;
+    }
+    if (act == GK_ACT_LEAKY_RELU && !std::isfinite(slope))
+        return fail(GK_ERR_ARG, "gemmkit: LeakyRelu slope must be finite");
+    return GK_OK;
+}
+
+int check_act_value(int32_t act) {
+    if (act != GK_ACT_NONE && act != GK_ACT_RELU && act != GK_ACT_LEAKY_RELU)
+        return fail(GK_ERR_ARG,
+                    "gemmkit: activation (%d) must be 0 (none), 1 (Relu) or 2 (LeakyRelu)", act);
+    return GK_OK;
+}
+
+// ---- prepacked float operands (src/api/packed.rs:67-170, :175-365)
+
+const char *in_name(InType t) {
+    return t == InType::I8 ? "i8" : (t == InType::BF16 ? "bf16" : "f32");
+}
+
+int check_packed(const gk_packed_rhs *p, InType want) {
+    if (!p) return fail(GK_ERR_ARG, "gemmkit: null packed RHS");
+    if (p->in != want)
+        return fail(GK_ERR_ARG, "gemmkit: packed RHS holds %s elements, this entry takes %s",
+                    in_name(p->in), in_name(want));
+    return GK_OK;
+}
+
+// prepack_rhs_unchecked (src/api/packed.rs:80-170): B^T (n x k) stored
+// k-contiguous in an owned device buffer, rows padded to 16 bytes with zeros.
+int prepack_any(InType in, const void *b, ptrdiff_t rsb, ptrdiff_t csb, size_t k, size_t n,
+                gk_packed_rhs **out) {
+    int r;
+    if (!out) return fail(GK_ERR_ARG, "gemmkit: null output handle");
+    *out = nullptr;
+    if ((r = device_init())) return r;
+    if (!dims_fit(1, k, n, 1))
+        return fail(GK_ERR_OVERFLOW,
+                    "gemmkit: prepacked RHS of %zux%zu is too large; the pack buffer size "
+                    "overflows usize",
+                    k, n);
+    const int64_t esz = (int64_t)in_size(in);
+    gk_packed_rhs *p = new gk_packed_rhs();
+    p->in = in;
+    p->k = k;
+    p->n = n;
+    p->ld = round_up64(std::max<int64_t>((int64_t)k, 1), 16 / esz);
+    if (k > 0 && n > 0) {
+        size_t bytes = (size_t)p->ld * n * (size_t)esz;
+        hipError_t e = hipMalloc(&p->buf, bytes);
+        if (e != hipSuccess) {
+            delete p;
+            return fail(GK_ERR_NOMEM, "gemmkit: prepacked RHS allocation of %zu bytes failed", bytes);
+        }
+        // Row j of the buffer is column j of B.
+        e = launch_pack(in, b, csb, rsb, (int64_t)n, (int64_t)k, p->buf, p->ld, tl_stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(tl_stream);
+        if (e != hipSuccess) {
+            (void)hipFree(p->buf);
+            delete p;
+            return hip_fail(e, "prepack");
+        }
+    }
+    *out = p;
+    return ok();
+}
+
+// gemm_packed_b_unchecked's orientation assert (src/api/packed.rs:625-629).
+int check_packed_c_layout(ptrdiff_t rsc, ptrdiff_t csc) {
+    if ((csc < 0 ? -csc : csc) < (rsc < 0 ? -rsc : rsc))
+        return fail(GK_ERR_LAYOUT,
+                    "gemmkit: gemm_packed_b requires column-major-ish C (|csc| >= |rsc|); a "
+                    "row-major C would swap A/B and invalidate the prepacked RHS \xE2\x80\x94 use "
+                    "gemm() for that layout");
+    return GK_OK;
+}
+
+// gemm_packed_b_with's checks (src/api/packed.rs:191-245): shapes against the
+// packed geometry, A and C in bounds, C addresses each element once, C clear
+// of A.  `sa`/`so`: A and C element sizes.
+int validate_packed_views(const gk_mat_ref *a, const gk_packed_rhs *packed, const gk_mat_mut *c,
+                          size_t sa, size_t so) {
+    if (!a || !c || !packed) return fail(GK_ERR_ARG, "gemmkit: null argument");
+    if (a->cols != packed->k)
+        return fail(GK_ERR_SHAPE, "gemmkit: A.cols (%zu) != packed B.rows (%zu)", a->cols, packed->k);
+    if (packed->n != c->cols)
+        return fail(GK_ERR_SHAPE, "gemmkit: packed B.cols (%zu) != C.cols (%zu)", packed->n, c->cols);
+    if (a->rows != c->rows)
+        return fail(GK_ERR_SHAPE, "gemmkit: A.rows (%zu) != C.rows (%zu)", a->rows, c->rows);
+    int r;
+    if ((r = check_view(a->len, a->rows, a->cols, a->rs, a->cs, "A"))) return r;
+    if ((r = check_view(c->len, c->rows, c->cols, c->rs, c->cs, "C"))) return r;
+    if (self_aliases(c->rows, c->cols, c->rs, c->cs))
+        return fail(GK_ERR_ALIAS,
+                    "gemmkit: C view aliases itself (strides %td,%td map distinct elements to the "
+                    "same memory); C must address each (i,j) uniquely",
+                    c->rs, c->cs);
+    if (overlaps_bytes(c->data, c->len, so, a->data, a->len, sa))
+        return fail(GK_ERR_ALIAS, "gemmkit: C aliases A");
+    return GK_OK;
+}
+
+// ---- fused / prepacked float entries, shared by the f32 and bf16 ABI twins.
+// `in`/`kind`: element type and output epilogue; `esz`: element size; scalars
+// already widened to f32.
+
+int fused_checked(gk_workspace *ws, InType in, EpiKind kind, size_t esz, float alpha,
+                  const gk_mat_ref *a, const gk_mat_ref *b, float beta, const gk_mat_mut *c,
+                  const gk_bias *bias, int32_t act, float slope) {
+    int r;
+    if ((r = check_act_value(act))) return r;
+    if ((r = validate_gemm_views(a, b, c, esz, esz))) return r;
+    FusedSpec fx;
+    if (bias || act != GK_ACT_NONE) {
+        if ((r = lower_fused(bias, act, slope, a->rows, b->cols, c, esz, esz, &fx))) return r;
+    }
+    // No bias and no activation: the plain GEMM (gemm_fused_with delegates to
+    // gemm_with, src/api/fused.rs:93-96).
+    return exec_float(ws, in, kind, 1, a->rows, a->cols, b->cols, alpha, a->data, a->rs, a->cs,
+                      0, b->data, b->rs, b->cs, 0, beta, c->data, c->rs, c->cs, 0,
+                      (bias || act != GK_ACT_NONE) ? &fx : nullptr);
+}
+
+int batched_fused_checked(gk_workspace *ws, InType in, EpiKind kind, size_t esz, size_t batch,
+                          float alpha, const gk_mat_ref *a, ptrdiff_t a_bs, const gk_mat_ref *b,
+                          ptrdiff_t b_bs, float beta, const gk_mat_mut *c, ptrdiff_t c_bs,
+                          const gk_bias *bias, int32_t act, float slope) {
+    int r;
+    if ((r = check_act_value(act))) return r;
+    if (batch == 0) return ok();
+    if ((r = validate_batched_views(batch, a, a_bs, b, b_bs, c, c_bs, esz, esz))) return r;
+    FusedSpec fx;
+    const bool any = bias || act != GK_ACT_NONE;
+    if (any && (r = lower_fused(bias, act, slope, a->rows, b->cols, c, esz, esz, &fx))) return r;
+    return exec_float(ws, in, kind, batch, a->rows, a->cols, b->cols, alpha, a->data, a->rs,
+                      a->cs, a_bs, b->data, b->rs, b->cs, b_bs, beta, c->data, c->rs, c->cs, c_bs,
+                      any ? &fx : nullptr);
+}
+
+int packed_b_unchecked(gk_workspace *ws, InType in, EpiKind kind, float alpha, size_t m,
+                       const void *a, ptrdiff_t rsa, ptrdiff_t csa, const gk_packed_rhs *packed,
+                       float beta, void *c, ptrdiff_t rsc, ptrdiff_t csc, const FusedSpec *fx) {
+    int r;
+    if ((r = check_packed(packed, in))) return r;
+    if ((r = check_packed_c_layout(rsc, csc))) return r;
+    return exec_float(ws, in, kind, 1, m, packed->k, packed->n, alpha, a, rsa, csa, 0, nullptr, 0,
+                      0, 0, beta, c, rsc, csc, 0, fx, packed);
+}
+
+int packed_b_checked(gk_workspace *ws, InType in, EpiKind kind, size_t esz, float alpha,
+                     const gk_mat_ref *a, const gk_packed_rhs *packed, float beta,
+                     const gk_mat_mut *c, bool fused, const gk_bias *bias, int32_t act,
+                     float slope) {
+    int r;
+    if (fused && (r = check_act_value(act))) return r;
+    if ((r = validate_packed_views(a, packed, c, esz, esz))) return r;
+    if ((r = check_packed(packed, in))) return r;
+    FusedSpec fx;
+    const bool any = fused && (bias || act != GK_ACT_NONE);
+    if (any && (r = lower_fused(bias, act, slope, a->rows, packed->n, c, esz, esz, &fx))) return r;
+    return packed_b_unchecked(ws, in, kind, alpha, a->rows, a->data, a->rs, a->cs, packed, beta,
+                              c->data, c->rs, c->cs, any ? &fx : nullptr);
+}
+
 }  // namespace
 
 // =============================================================== C ABI
@@ -897,33 +1128,7 @@ int gk_gemm_i8_requant_u8_unchecked(gk_workspace *ws, size_t m, size_t k, size_t
 
 int gk_prepack_rhs_i8_unchecked(const int8_t *b, ptrdiff_t rsb, ptrdiff_t csb, size_t k, size_t n,
                                 gk_packed_rhs **out) {
-    int r;
-    if (!out) return fail(GK_ERR_ARG, "gemmkit: null output handle");
-    *out = nullptr;
-    if ((r = device_init())) return r;
-    if (!dims_fit(1, k, n, 1)) return fail(GK_ERR_OVERFLOW, "gemmkit: prepacked RHS of %zux%zu is too large; the pack buffer size overflows usize", k, n);
-    gk_packed_rhs *p = new gk_packed_rhs();
-    p->k = k;
-    p->n = n;
-    p->ld = round_up64(std::max<int64_t>((int64_t)k, 1), 16);
-    if (k > 0 && n > 0) {
-        size_t bytes = (size_t)p->ld * n;
-        hipError_t e = hipMalloc((void **)&p->buf, bytes);
-        if (e != hipSuccess) {
-            delete p;
-            return fail(GK_ERR_NOMEM, "gemmkit: prepacked RHS allocation of %zu bytes failed", bytes);
-        }
-        // Store B^T (n x k) k-contiguous: row j of the buffer is column j of B.
-        e = launch_pack(InType::I8, b, csb, rsb, (int64_t)n, (int64_t)k, p->buf, p->ld, tl_stream);
-        if (e == hipSuccess) e = hipStreamSynchronize(tl_stream);
-        if (e != hipSuccess) {
-            (void)hipFree(p->buf);
-            delete p;
-            return hip_fail(e, "prepack");
-        }
-    }
-    *out = p;
-    return ok();
+    return prepack_any(InType::I8, b, rsb, csb, k, n, out);
 }
 
 int gk_prepack_rhs_i8(const gk_mat_ref *b, gk_packed_rhs **out) {
@@ -931,6 +1136,30 @@ int gk_prepack_rhs_i8(const gk_mat_ref *b, gk_packed_rhs **out) {
     int r = check_view(b->len, b->rows, b->cols, b->rs, b->cs, "B");
     if (r) return r;
     return gk_prepack_rhs_i8_unchecked((const int8_t *)b->data, b->rs, b->cs, b->rows, b->cols, out);
+}
+
+int gk_prepack_rhs_f32_unchecked(const float *b, ptrdiff_t rsb, ptrdiff_t csb, size_t k, size_t n,
+                                 gk_packed_rhs **out) {
+    return prepack_any(InType::F32, b, rsb, csb, k, n, out);
+}
+
+int gk_prepack_rhs_f32(const gk_mat_ref *b, gk_packed_rhs **out) {
+    if (!b) return fail(GK_ERR_ARG, "gemmkit: null view argument");
+    int r = check_view(b->len, b->rows, b->cols, b->rs, b->cs, "B");
+    if (r) return r;
+    return prepack_any(InType::F32, b->data, b->rs, b->cs, b->rows, b->cols, out);
+}
+
+int gk_prepack_rhs_bf16_unchecked(const gk_bf16 *b, ptrdiff_t rsb, ptrdiff_t csb, size_t k,
+                                  size_t n, gk_packed_rhs **out) {
+    return prepack_any(InType::BF16, b, rsb, csb, k, n, out);
+}
+
+int gk_prepack_rhs_bf16(const gk_mat_ref *b, gk_packed_rhs **out) {
+    if (!b) return fail(GK_ERR_ARG, "gemmkit: null view argument");
+    int r = check_view(b->len, b->rows, b->cols, b->rs, b->cs, "B");
+    if (r) return r;
+    return prepack_any(InType::BF16, b->data, b->rs, b->cs, b->rows, b->cols, out);
 }
 
 void gk_packed_rhs_free(gk_packed_rhs *p) {
@@ -948,13 +1177,9 @@ size_t gk_packed_rhs_cols(const gk_packed_rhs *p) { return p ? p->n : 0; }
 int gk_gemm_i8_packed_b_unchecked(gk_workspace *ws, int32_t alpha, size_t m, const int8_t *a,
                                   ptrdiff_t rsa, ptrdiff_t csa, const gk_packed_rhs *packed,
                                   int32_t beta, int32_t *c, ptrdiff_t rsc, ptrdiff_t csc, gk_par) {
-    if (!packed) return fail(GK_ERR_ARG, "gemmkit: null packed RHS");
-    // Same orientation rule as the reference (src/api/packed.rs:625-629).
-    if ((csc < 0 ? -csc : csc) < (rsc < 0 ? -rsc : rsc))
-        return fail(GK_ERR_LAYOUT,
-                    "gemmkit: gemm_packed_b requires column-major-ish C (|csc| >= |rsc|); a "
-                    "row-major C would swap A/B and invalidate the prepacked RHS \xE2\x80\x94 use "
-                    "gemm() for that layout");
+    int r;
+    if ((r = check_packed(packed, InType::I8))) return r;
+    if ((r = check_packed_c_layout(rsc, csc))) return r;
     return exec_i8(ws, m, packed->k, packed->n, alpha, a, rsa, csa, nullptr, 0, 0, beta, c, rsc,
                    csc, packed);
 }
@@ -962,37 +1187,23 @@ int gk_gemm_i8_packed_b_unchecked(gk_workspace *ws, int32_t alpha, size_t m, con
 int gk_gemm_i8_packed_b(gk_workspace *ws, int32_t alpha, const gk_mat_ref *a,
                         const gk_packed_rhs *packed, int32_t beta, const gk_mat_mut *c,
                         gk_par par) {
-    if (!a || !c || !packed) return fail(GK_ERR_ARG, "gemmkit: null argument");
-    if (a->cols != packed->k)
-        return fail(GK_ERR_SHAPE, "gemmkit: A.cols (%zu) != packed B.rows (%zu)", a->cols, packed->k);
-    if (packed->n != c->cols)
-        return fail(GK_ERR_SHAPE, "gemmkit: packed B.cols (%zu) != C.cols (%zu)", packed->n, c->cols);
-    if (a->rows != c->rows)
-        return fail(GK_ERR_SHAPE, "gemmkit: A.rows (%zu) != C.rows (%zu)", a->rows, c->rows);
     int r;
-    if ((r = check_view(a->len, a->rows, a->cols, a->rs, a->cs, "A"))) return r;
-    if ((r = check_view(c->len, c->rows, c->cols, c->rs, c->cs, "C"))) return r;
-    if (self_aliases(c->rows, c->cols, c->rs, c->cs))
-        return fail(GK_ERR_ALIAS,
-                    "gemmkit: C view aliases itself (strides %td,%td map distinct elements to the "
-                    "same memory); C must address each (i,j) uniquely",
-                    c->rs, c->cs);
-    if (overlaps_bytes(c->data, c->len, 4, a->data, a->len, 1))
-        return fail(GK_ERR_ALIAS, "gemmkit: C aliases A");
+    if ((r = validate_packed_views(a, packed, c, 1, 4))) return r;
+    if ((r = check_packed(packed, InType::I8))) return r;
     return gk_gemm_i8_packed_b_unchecked(ws, alpha, a->rows, (const int8_t *)a->data, a->rs, a->cs,
                                          packed, beta, (int32_t *)c->data, c->rs, c->cs, par);
 }
 
 int gk_gemm_i8_packed_b_requant(gk_workspace *ws, const gk_mat_ref *a, const gk_packed_rhs *packed,
                                 const gk_requantize *req, const gk_mat_mut *c, gk_par) {
-    if (!packed) return fail(GK_ERR_ARG, "gemmkit: null packed RHS");
+    if (int r = check_packed(packed, InType::I8)) return r;
     return requant_checked(ws, a, nullptr, packed, req, c, false);
 }
 
 int gk_gemm_i8_packed_b_requant_u8(gk_workspace *ws, const gk_mat_ref *a,
                                    const gk_packed_rhs *packed, const gk_requantize *req,
                                    const gk_mat_mut *c, gk_par) {
-    if (!packed) return fail(GK_ERR_ARG, "gemmkit: null packed RHS");
+    if (int r = check_packed(packed, InType::I8)) return r;
     return requant_checked(ws, a, nullptr, packed, req, c, true);
 }
 
@@ -1003,7 +1214,7 @@ int gk_gemm_i8_packed_b_requant_unchecked(gk_workspace *ws, size_t m, const int8
                                           int32_t zero_point, const int32_t *bias,
                                           uint8_t has_bias, int8_t *c, ptrdiff_t rsc,
                                           ptrdiff_t csc, gk_par, int32_t axis, int32_t act) {
-    if (!packed) return fail(GK_ERR_ARG, "gemmkit: null packed RHS");
+    if (int r = check_packed(packed, InType::I8)) return r;
     return exec_requant(ws, m, packed->k, packed->n, a, rsa, csa, nullptr, 0, 0, scale,
                         has_scales ? scales : nullptr, zero_point, has_bias ? bias : nullptr, axis,
                         act, -128, 127, c, rsc, csc, packed);
@@ -1016,7 +1227,7 @@ int gk_gemm_i8_packed_b_requant_u8_unchecked(gk_workspace *ws, size_t m, const i
                                              int32_t zero_point, const int32_t *bias,
                                              uint8_t has_bias, uint8_t *c, ptrdiff_t rsc,
                                              ptrdiff_t csc, gk_par, int32_t axis, int32_t act) {
-    if (!packed) return fail(GK_ERR_ARG, "gemmkit: null packed RHS");
+    if (int r = check_packed(packed, InType::I8)) return r;
     return exec_requant(ws, m, packed->k, packed->n, a, rsa, csa, nullptr, 0, 0, scale,
                         has_scales ? scales : nullptr, zero_point, has_bias ? bias : nullptr, axis,
                         act, 0, 255, c, rsc, csc, packed);
@@ -1086,6 +1297,149 @@ int gk_gemm_batched_bf16_f32out(gk_workspace *ws, size_t batch, float alpha, con
                                                  (const gk_bf16 *)a->data, a->rs, a->cs, a_bs,
                                                  (const gk_bf16 *)b->data, b->rs, b->cs, b_bs,
                                                  beta, (float *)c->data, c->rs, c->cs, c_bs, par);
+}
+
+// ---- prepacked float RHS (src/api/packed.rs:175-365)
+
+int gk_gemm_packed_b_f32_unchecked(gk_workspace *ws, float alpha, size_t m, const float *a,
+                                   ptrdiff_t rsa, ptrdiff_t csa, const gk_packed_rhs *packed,
+                                   float beta, float *c, ptrdiff_t rsc, ptrdiff_t csc, gk_par) {
+    return packed_b_unchecked(ws, InType::F32, EpiKind::F32, alpha, m, a, rsa, csa, packed, beta,
+                              c, rsc, csc, nullptr);
+}
+
+int gk_gemm_packed_b_f32(gk_workspace *ws, float alpha, const gk_mat_ref *a,
+                         const gk_packed_rhs *packed, float beta, const gk_mat_mut *c, gk_par) {
+    return packed_b_checked(ws, InType::F32, EpiKind::F32, 4, alpha, a, packed, beta, c, false,
+                            nullptr, GK_ACT_NONE, 0.0f);
+}
+
+int gk_gemm_packed_b_bf16_unchecked(gk_workspace *ws, gk_bf16 alpha, size_t m, const gk_bf16 *a,
+                                    ptrdiff_t rsa, ptrdiff_t csa, const gk_packed_rhs *packed,
+                                    gk_bf16 beta, gk_bf16 *c, ptrdiff_t rsc, ptrdiff_t csc,
+                                    gk_par) {
+    return packed_b_unchecked(ws, InType::BF16, EpiKind::BF16, bf16_to_f32(alpha), m, a, rsa, csa,
+                              packed, bf16_to_f32(beta), c, rsc, csc, nullptr);
+}
+
+int gk_gemm_packed_b_bf16(gk_workspace *ws, gk_bf16 alpha, const gk_mat_ref *a,
+                          const gk_packed_rhs *packed, gk_bf16 beta, const gk_mat_mut *c, gk_par) {
+    return packed_b_checked(ws, InType::BF16, EpiKind::BF16, 2, bf16_to_f32(alpha), a, packed,
+                            bf16_to_f32(beta), c, false, nullptr, GK_ACT_NONE, 0.0f);
+}
+
+// ---- fused bias / activation (src/api/fused.rs, src/api/batched.rs:307-590,
+// src/api/packed.rs:684-950)
+
+int gk_gemm_fused_f32(gk_workspace *ws, float alpha, const gk_mat_ref *a, const gk_mat_ref *b,
+                      float beta, const gk_mat_mut *c, const gk_bias *bias, int32_t act,
+                      float slope, gk_par) {
+    return fused_checked(ws, InType::F32, EpiKind::F32, 4, alpha, a, b, beta, c, bias, act, slope);
+}
+
+int gk_gemm_fused_f32_unchecked(gk_workspace *ws, size_t m, size_t k, size_t n, float alpha,
+                                const float *a, ptrdiff_t rsa, ptrdiff_t csa, const float *b,
+                                ptrdiff_t rsb, ptrdiff_t csb, float beta, float *c, ptrdiff_t rsc,
+                                ptrdiff_t csc, const float *bias, int32_t bias_dim,
+                                uint8_t has_bias, int32_t act, float slope, gk_par) {
+    const FusedSpec fx{has_bias ? bias : nullptr, bias_dim, act, slope};
+    return exec_float(ws, InType::F32, EpiKind::F32, 1, m, k, n, alpha, a, rsa, csa, 0, b, rsb,
+                      csb, 0, beta, c, rsc, csc, 0, &fx);
+}
+
+int gk_gemm_fused_bf16(gk_workspace *ws, gk_bf16 alpha, const gk_mat_ref *a, const gk_mat_ref *b,
+                       gk_bf16 beta, const gk_mat_mut *c, const gk_bias *bias, int32_t act,
+                       gk_bf16 slope, gk_par) {
+    return fused_checked(ws, InType::BF16, EpiKind::BF16, 2, bf16_to_f32(alpha), a, b,
+                         bf16_to_f32(beta), c, bias, act, bf16_to_f32(slope));
+}
+
+int gk_gemm_fused_bf16_unchecked(gk_workspace *ws, size_t m, size_t k, size_t n, gk_bf16 alpha,
+                                 const gk_bf16 *a, ptrdiff_t rsa, ptrdiff_t csa, const gk_bf16 *b,
+                                 ptrdiff_t rsb, ptrdiff_t csb, gk_bf16 beta, gk_bf16 *c,
+                                 ptrdiff_t rsc, ptrdiff_t csc, const gk_bf16 *bias,
+                                 int32_t bias_dim, uint8_t has_bias, int32_t act, gk_bf16 slope,
+                                 gk_par) {
+    const FusedSpec fx{has_bias ? bias : nullptr, bias_dim, act, bf16_to_f32(slope)};
+    return exec_float(ws, InType::BF16, EpiKind::BF16, 1, m, k, n, bf16_to_f32(alpha), a, rsa, csa,
+                      0, b, rsb, csb, 0, bf16_to_f32(beta), c, rsc, csc, 0, &fx);
+}
+
+int gk_gemm_batched_fused_f32(gk_workspace *ws, size_t batch, float alpha, const gk_mat_ref *a,
+                              ptrdiff_t a_bs, const gk_mat_ref *b, ptrdiff_t b_bs, float beta,
+                              const gk_mat_mut *c, ptrdiff_t c_bs, const gk_bias *bias,
+                              int32_t act, float slope, gk_par) {
+    return batched_fused_checked(ws, InType::F32, EpiKind::F32, 4, batch, alpha, a, a_bs, b, b_bs,
+                                 beta, c, c_bs, bias, act, slope);
+}
+
+int gk_gemm_batched_fused_f32_unchecked(gk_workspace *ws, size_t batch, size_t m, size_t k,
+                                        size_t n, float alpha, const float *a, ptrdiff_t rsa,
+                                        ptrdiff_t csa, ptrdiff_t a_bs, const float *b,
+                                        ptrdiff_t rsb, ptrdiff_t csb, ptrdiff_t b_bs, float beta,
+                                        float *c, ptrdiff_t rsc, ptrdiff_t csc, ptrdiff_t c_bs,
+                                        const float *bias, int32_t bias_dim, uint8_t has_bias,
+                                        int32_t act, float slope, gk_par) {
+    const FusedSpec fx{has_bias ? bias : nullptr, bias_dim, act, slope};
+    return exec_float(ws, InType::F32, EpiKind::F32, batch, m, k, n, alpha, a, rsa, csa, a_bs, b,
+                      rsb, csb, b_bs, beta, c, rsc, csc, c_bs, &fx);
+}
+
+int gk_gemm_batched_fused_bf16(gk_workspace *ws, size_t batch, gk_bf16 alpha,
+                               const gk_mat_ref *a, ptrdiff_t a_bs, const gk_mat_ref *b,
+                               ptrdiff_t b_bs, gk_bf16 beta, const gk_mat_mut *c, ptrdiff_t c_bs,
+                               const gk_bias *bias, int32_t act, gk_bf16 slope, gk_par) {
+    return batched_fused_checked(ws, InType::BF16, EpiKind::BF16, 2, batch, bf16_to_f32(alpha), a,
+                                 a_bs, b, b_bs, bf16_to_f32(beta), c, c_bs, bias, act,
+                                 bf16_to_f32(slope));
+}
+
+int gk_gemm_batched_fused_bf16_unchecked(gk_workspace *ws, size_t batch, size_t m, size_t k,
+                                         size_t n, gk_bf16 alpha, const gk_bf16 *a, ptrdiff_t rsa,
+                                         ptrdiff_t csa, ptrdiff_t a_bs, const gk_bf16 *b,
+                                         ptrdiff_t rsb, ptrdiff_t csb, ptrdiff_t b_bs,
+                                         gk_bf16 beta, gk_bf16 *c, ptrdiff_t rsc, ptrdiff_t csc,
+                                         ptrdiff_t c_bs, const gk_bf16 *bias, int32_t bias_dim,
+                                         uint8_t has_bias, int32_t act, gk_bf16 slope, gk_par) {
+    const FusedSpec fx{has_bias ? bias : nullptr, bias_dim, act, bf16_to_f32(slope)};
+    return exec_float(ws, InType::BF16, EpiKind::BF16, batch, m, k, n, bf16_to_f32(alpha), a, rsa,
+                      csa, a_bs, b, rsb, csb, b_bs, bf16_to_f32(beta), c, rsc, csc, c_bs, &fx);
+}
+
+int gk_gemm_packed_b_fused_f32(gk_workspace *ws, float alpha, const gk_mat_ref *a,
+                               const gk_packed_rhs *packed, float beta, const gk_mat_mut *c,
+                               const gk_bias *bias, int32_t act, float slope, gk_par) {
+    return packed_b_checked(ws, InType::F32, EpiKind::F32, 4, alpha, a, packed, beta, c, true,
+                            bias, act, slope);
+}
+
+int gk_gemm_packed_b_fused_f32_unchecked(gk_workspace *ws, float alpha, size_t m, const float *a,
+                                         ptrdiff_t rsa, ptrdiff_t csa,
+                                         const gk_packed_rhs *packed, float beta, float *c,
+                                         ptrdiff_t rsc, ptrdiff_t csc, const float *bias,
+                                         int32_t bias_dim, uint8_t has_bias, int32_t act,
+                                         float slope, gk_par) {
+    const FusedSpec fx{has_bias ? bias : nullptr, bias_dim, act, slope};
+    return packed_b_unchecked(ws, InType::F32, EpiKind::F32, alpha, m, a, rsa, csa, packed, beta,
+                              c, rsc, csc, &fx);
+}
+
+int gk_gemm_packed_b_fused_bf16(gk_workspace *ws, gk_bf16 alpha, const gk_mat_ref *a,
+                                const gk_packed_rhs *packed, gk_bf16 beta, const gk_mat_mut *c,
+                                const gk_bias *bias, int32_t act, gk_bf16 slope, gk_par) {
+    return packed_b_checked(ws, InType::BF16, EpiKind::BF16, 2, bf16_to_f32(alpha), a, packed,
+                            bf16_to_f32(beta), c, true, bias, act, bf16_to_f32(slope));
+}
+
+int gk_gemm_packed_b_fused_bf16_unchecked(gk_workspace *ws, gk_bf16 alpha, size_t m,
+                                          const gk_bf16 *a, ptrdiff_t rsa, ptrdiff_t csa,
+                                          const gk_packed_rhs *packed, gk_bf16 beta, gk_bf16 *c,
+                                          ptrdiff_t rsc, ptrdiff_t csc, const gk_bf16 *bias,
+                                          int32_t bias_dim, uint8_t has_bias, int32_t act,
+                                          gk_bf16 slope, gk_par) {
+    const FusedSpec fx{has_bias ? bias : nullptr, bias_dim, act, bf16_to_f32(slope)};
+    return packed_b_unchecked(ws, InType::BF16, EpiKind::BF16, bf16_to_f32(alpha), m, a, rsa, csa,
+                              packed, bf16_to_f32(beta), c, rsc, csc, &fx);
 }
 
 }  // extern "C"

@@ -13,6 +13,8 @@
 //        one f64 multiply by the widened f32 scale, round half to even, zero
 //        point, clamp to [lo, hi], store the low byte -- computed exactly
 //        without f64 arithmetic (requant.h).
+// F32 and BF16 also carry gemmkit's fused bias/activation (FusedEpi,
+// src/kernel/epilogue.rs:269-330 and :556-596) on the f32 value before the store.
 #pragma once
 
 #include "internal.h"
@@ -38,6 +40,35 @@ __device__ __forceinline__ float bf16_widen(uint16_t h) {
 __device__ __forceinline__ int32_t requant_value(int32_t acc, int32_t bias, float scale,
                                                  int32_t zp, int32_t lo, int32_t hi) {
     return requant_fast(acc, bias, scale, zp, lo, hi);
+}
+
+// FusedEpi::apply (src/kernel/epilogue.rs:309-330, :569-596) on the f32 value
+// the plain store would write, with the bias value b already loaded (0 when
+// there is no bias: v + 0 differs from v only for v = -0, which every
+// activation maps to +0, and the map is off when there is neither).  ReLU is
+// v > 0 ? v : 0, so NaN and -0 give +0; LeakyReLU is hi + slope*lo with
+// hi = v > 0 ? v : 0 and lo = v < 0 ? v : 0.  Nothing here may contract into
+// an FMA, which keeps f32 results bit-identical to the plain GEMM followed by
+// the same scalar map.
+__device__ __forceinline__ float fused_apply(const EpiParams &ep, float v, float b) {
+#pragma clang fp contract(off)
+    v = v + b;
+    const float hi = v > 0.0f ? v : 0.0f;
+    const float lo = v < 0.0f ? v : 0.0f;
+    const float leaky = hi + ep.slope * lo;
+    return ep.act == kActRelu ? hi : (ep.act == kActLeakyRelu ? leaky : v);
+}
+
+// The bias value of channel ch: f32, or bf16 widened exactly when BF16_BIAS.
+template <bool BF16_BIAS>
+__device__ __forceinline__ float fused_bias(const EpiParams &ep, int ch) {
+    if (!ep.fbias) return 0.0f;
+    return BF16_BIAS ? bf16_widen(((const uint16_t *)ep.fbias)[ch]) : ((const float *)ep.fbias)[ch];
+}
+
+template <bool BF16_BIAS>
+__device__ __forceinline__ float fused_map(const EpiParams &ep, float v, int row, int col) {
+    return fused_apply(ep, v, fused_bias<BF16_BIAS>(ep, ep.axis ? col : row));
 }
 
 // Stores one accumulator at output coordinate (row, col) of batch element z.
@@ -66,13 +97,13 @@ struct Store<EpiKind::F32> {
                                                  float acc) {
         float *c = (float *)ep.c + z * ep.bsc + (int64_t)row * ep.rsc + (int64_t)col * ep.csc;
         float v = ep.alpha_f * acc;
-        if (ep.beta_f == 0.0f) {
-            *c = v;
-        } else if (ep.beta_f == 1.0f) {
-            *c = *c + v;
-        } else {
-            *c = __builtin_fmaf(ep.beta_f, *c, v);
+        if (ep.beta_f == 1.0f) {
+            v = *c + v;
+        } else if (ep.beta_f != 0.0f) {
+            v = __builtin_fmaf(ep.beta_f, *c, v);
         }
+        if (ep.fused) v = fused_map<false>(ep, v, row, col);
+        *c = v;
     }
 };
 
@@ -87,6 +118,7 @@ struct Store<EpiKind::BF16> {
         } else if (ep.beta_f != 0.0f) {
             v = __builtin_fmaf(ep.beta_f, bf16_widen(*c), v);
         }
+        if (ep.fused) v = fused_map<true>(ep, v, row, col);
         *c = bf16_rne(v);
     }
 };
@@ -112,10 +144,11 @@ struct Store<EpiKind::Q8> {
 // Requantization uses the caller's per-element channel scale and bias (qs,
 // qb): the f32 path for all four, and the exact integer path for every lane
 // of the wave when any lane needs it.
+// For F32/BF16 with a fused epilogue, fb holds the four elements' bias values.
 template <EpiKind K, typename A>
 __device__ __forceinline__ void store4(const EpiParams &ep, int64_t z, int row, int col, int ncols,
                                        const A v[4], const float *qs = nullptr,
-                                       const int32_t *qb = nullptr) {
+                                       const int32_t *qb = nullptr, const float *fb = nullptr) {
     const int nvalid = ncols - col < 4 ? ncols - col : 4;
     int32_t q[4] = {0, 0, 0, 0};
     if constexpr (K == EpiKind::Q8) {
@@ -169,6 +202,9 @@ __device__ __forceinline__ void store4(const EpiParams &ep, int64_t z, int row, 
             for (int e = 0; e < 4; ++e)
                 o[e] = ep.beta_f == 1.0f ? old[e] + o[e] : __builtin_fmaf(ep.beta_f, old[e], o[e]);
         }
+        if (ep.fused) {
+            for (int e = 0; e < 4; ++e) o[e] = fused_apply(ep, o[e], fb[e]);
+        }
         __builtin_nontemporal_store(o, c);
     } else if constexpr (K == EpiKind::BF16) {
         typedef uint32_t v2u_e __attribute__((ext_vector_type(2)));
@@ -181,6 +217,9 @@ __device__ __forceinline__ void store4(const EpiParams &ep, int64_t z, int row, 
                 float w = bf16_widen((uint16_t)(old[e >> 1] >> (16 * (e & 1))));
                 f[e] = ep.beta_f == 1.0f ? w + f[e] : __builtin_fmaf(ep.beta_f, w, f[e]);
             }
+        }
+        if (ep.fused) {
+            for (int e = 0; e < 4; ++e) f[e] = fused_apply(ep, f[e], fb[e]);
         }
         v2u_e o;
         o[0] = (uint32_t)bf16_rne(f[0]) | ((uint32_t)bf16_rne(f[1]) << 16);

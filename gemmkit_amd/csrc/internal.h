@@ -5,7 +5,7 @@
 // lives at base + r*ld + p, rows 16-byte aligned, K*sizeof(T) a multiple of 16.
 // That is the layout gemmkit's packers produce for its microkernels
 // (src/pack.rs:28-117): the contraction index is the fast one.  The host
-// dispatcher (dispatch.cpp) brings every call into this frame with the
+// dispatcher (capi.cpp) brings every call into this frame with the
 // reference's orientation swap (src/dispatch.rs:395-417) -- free here because
 // both operands are k-contiguous -- and packs an operand into the workspace
 // only when its own strides are not k-contiguous.
@@ -37,7 +37,17 @@ struct EpiParams {
     int32_t axis;          // 0: channel = kernel row, 1: channel = kernel column
     int32_t zp, lo, hi;    // zero point and clamp band (ReLU already folded into lo)
     int32_t vec4;          // C is unit-stride along columns and 4-element aligned
+    // fused bias and activation (EpiKind::F32 / BF16, FusedEpi in
+    // src/kernel/epilogue.rs:269-330): v <- act(v + fbias[channel]) on the f32
+    // value the plain store would write, channel along `axis`; fbias holds f32
+    // for F32 output and bf16 for BF16 output.
+    int32_t fused;         // fbias != nullptr || act != kActNone
+    int32_t act;           // FusedAct
+    float slope;           // LeakyReLU slope (widened to f32)
+    const void *fbias;     // bias vector or nullptr
 };
+
+enum FusedAct : int32_t { kActNone = 0, kActRelu = 1, kActLeakyRelu = 2 };
 
 // Largest operand row stride and row length (bytes) the matrix-core kernels
 // address: 256 row strides plus a row stay below 2^31 bytes of 32-bit buffer
@@ -53,7 +63,7 @@ struct MmaArgs {
     int32_t batch;
 };
 
-// Tile shapes instantiated in mfma_gemm.hip.
+// Tile shapes instantiated in mfma_{i8,bf16,f32}.hip.
 enum class Tile : int {
     T256x256 = 0,
     T256x128 = 1,
@@ -101,5 +111,11 @@ hipError_t launch_scale_c(EpiKind kind, void *c, int64_t m, int64_t n, int64_t r
 
 // k == 0 requant fill (requant_degenerate, src/dispatch/int.rs:735-752).
 hipError_t launch_requant_fill(const EpiParams &ep, int64_t m, int64_t n, hipStream_t stream);
+
+// Fused degenerate map C <- act(beta*C + bias) when the A*B term vanishes
+// (fused_degenerate_float, src/dispatch/float.rs:739-758; fused_degenerate_mixed,
+// src/dispatch/mixed.rs:490-512).  `ep` in the user frame, batch elements bsc apart.
+hipError_t launch_fused_fill(const EpiParams &ep, int64_t m, int64_t n, int64_t batch,
+                             hipStream_t stream);
 
 }  // namespace gk

@@ -404,10 +404,12 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     val_t *stg = (val_t *)smem + wave * 32 * EPI_LD;
     constexpr int CPRE = WTN / 4;          // 4-column chunks per staged row
     constexpr int RPIT = 64 / CPRE;        // rows per read iteration
-    // The requantizing store is long; unrolling its row loop fully would make
-    // the block loop too large to unroll, and the accumulator array would then
-    // be indexed at run time (scratch memory).
-    constexpr int IT_UNROLL = (E == EpiKind::Q8) ? 4 : 32 / RPIT;
+    // The requantizing and the bf16 (narrowing, fused) stores are long;
+    // unrolling their row loop fully would make the block loop too large to
+    // unroll, and the accumulator array would then be indexed at run time
+    // (scratch memory).
+    constexpr int IT_UNROLL =
+        (E == EpiKind::Q8 || E == EpiKind::BF16) && 32 / RPIT > 4 ? 4 : 32 / RPIT;
     // Requantization channels of this lane's 4 columns (fixed for the whole
     // tile when they are columns).
     float col_s[4] = {0, 0, 0, 0};
@@ -420,6 +422,17 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
                 col_s[e] = q_scale[ci + e];
                 col_b[e] = q_bias[ci + e];
             }
+        }
+    }
+    // Fused bias values of this lane's 4 columns (per-column bias), likewise.
+    constexpr bool FB = E == EpiKind::F32 || E == EpiKind::BF16;
+    float col_f[4] = {0, 0, 0, 0};
+    if constexpr (FB) {
+        if (ep.fused && ep.axis) {
+            const int cf = n0 + wn * WTN + (lane % CPRE) * 4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                col_f[e] = cf + e < args.N ? fused_bias<E == EpiKind::BF16>(ep, cf + e) : 0.0f;
         }
     }
 #pragma unroll
@@ -456,8 +469,16 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
                     }
                 }
             }
+            float f4[4] = {col_f[0], col_f[1], col_f[2], col_f[3]};
+            if constexpr (FB) {
+                if (ep.fused && !ep.axis) {
+                    const float f = grow < args.M ? fused_bias<E == EpiKind::BF16>(ep, grow) : 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) f4[e] = f;
+                }
+            }
             if (grow < args.M && gcol0 + c4 < args.N)
-                store4<E, val_t>(ep, z, grow, gcol0 + c4, args.N, v, s4, b4);
+                store4<E, val_t>(ep, z, grow, gcol0 + c4, args.N, v, s4, b4, f4);
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_wave_barrier();

@@ -10,6 +10,8 @@
 //                    src/dispatch.rs:484-497; the narrow twin for bf16).
 //   requant_fill     the k == 0 requant fill (requant_degenerate,
 //                    src/dispatch/int.rs:735-752).
+//   fused_fill       C <- act(beta*C + bias) when the A*B term of a fused
+//                    call vanishes (src/dispatch/float.rs:661-680).
 #include "epilogue.h"
 
 namespace gk {
@@ -101,6 +103,38 @@ hipError_t launch_requant_fill(const EpiParams &ep, int64_t m, int64_t n, hipStr
     if (m == 0 || n == 0) return hipSuccess;
     dim3 grid((unsigned)((m * n + 255) / 256));
     hipLaunchKernelGGL(requant_fill_kernel, grid, dim3(256), 0, stream, ep, m, n);
+    return hipGetLastError();
+}
+
+// Fused degenerate map: one thread per element of a (batch x) m x n view in the
+// user frame.  beta*C stays a separate rounding before the bias add, as in the
+// reference's scalar loop.
+__global__ __launch_bounds__(256) void fused_fill_kernel(const EpiParams ep, int64_t m,
+                                                         int64_t n) {
+#pragma clang fp contract(off)
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t z = blockIdx.y;
+    if (idx >= m * n) return;
+    const int i = (int)(idx / n), j = (int)(idx % n);
+    const int64_t off = z * ep.bsc + (int64_t)i * ep.rsc + (int64_t)j * ep.csc;
+    if (ep.kind == EpiKind::F32) {
+        float *p = (float *)ep.c + off;
+        const float base = ep.beta_f == 0.0f ? 0.0f : (ep.beta_f == 1.0f ? *p : ep.beta_f * *p);
+        *p = fused_map<false>(ep, base, i, j);
+    } else {
+        uint16_t *p = (uint16_t *)ep.c + off;
+        const float base = ep.beta_f == 0.0f
+                               ? 0.0f
+                               : (ep.beta_f == 1.0f ? bf16_widen(*p) : ep.beta_f * bf16_widen(*p));
+        *p = bf16_rne(fused_map<true>(ep, base, i, j));
+    }
+}
+
+hipError_t launch_fused_fill(const EpiParams &ep, int64_t m, int64_t n, int64_t batch,
+                             hipStream_t stream) {
+    if (m == 0 || n == 0 || batch == 0) return hipSuccess;
+    dim3 grid((unsigned)((m * n + 255) / 256), (unsigned)batch);
+    hipLaunchKernelGGL(fused_fill_kernel, grid, dim3(256), 0, stream, ep, m, n);
     return hipGetLastError();
 }
 

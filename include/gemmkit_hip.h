@@ -168,6 +168,8 @@ int gk_gemm_i8_unchecked(gk_workspace *ws, size_t m, size_t k, size_t n, int32_t
  * max(0, real value) because round-half-even is monotone with rne(0) = 0. */
 #define GK_ACT_NONE 0
 #define GK_ACT_RELU 1
+/* Fused-epilogue entries only (Activation::LeakyRelu, src/api/fused.rs:26-31). */
+#define GK_ACT_LEAKY_RELU 2
 
 /* Requantize (src/api/int8.rs:185-209) plus the two extension fields.
  * scales == NULL selects RequantScale::PerTensor(scale); otherwise `scales`
@@ -267,6 +269,36 @@ int gk_gemm_i8_packed_b_requant_u8_unchecked(gk_workspace *ws, size_t m, const i
                                              ptrdiff_t csc, gk_par par, int32_t axis,
                                              int32_t act);
 
+/* ------------------------------------------------------ prepacked f32/bf16 RHS */
+
+/* prepack_rhs::<f32> / ::<bf16> (src/api/packed.rs:67) and prepack_rhs_unchecked
+ * (:80): the same opaque handle as the i8 pack, typed by its element; an entry
+ * given a handle of another element type returns GK_ERR_ARG. */
+int gk_prepack_rhs_f32(const gk_mat_ref *b, gk_packed_rhs **out);
+int gk_prepack_rhs_f32_unchecked(const float *b, ptrdiff_t rsb, ptrdiff_t csb, size_t k,
+                                 size_t n, gk_packed_rhs **out);
+int gk_prepack_rhs_bf16(const gk_mat_ref *b, gk_packed_rhs **out);
+int gk_prepack_rhs_bf16_unchecked(const gk_bf16 *b, ptrdiff_t rsb, ptrdiff_t csb, size_t k,
+                                  size_t n, gk_packed_rhs **out);
+
+/* gemm_packed_b::<f32|bf16> / _with (src/api/packed.rs:175, :191): results as
+ * gemm; a column-major-ish C (|csc| >= |rsc|) is required, as in the reference. */
+int gk_gemm_packed_b_f32(gk_workspace *ws, float alpha, const gk_mat_ref *a,
+                         const gk_packed_rhs *packed, float beta, const gk_mat_mut *c,
+                         gk_par par);
+/* gemm_packed_b_unchecked(_with) (src/api/packed.rs:270, :301). */
+int gk_gemm_packed_b_f32_unchecked(gk_workspace *ws, float alpha, size_t m, const float *a,
+                                   ptrdiff_t rsa, ptrdiff_t csa, const gk_packed_rhs *packed,
+                                   float beta, float *c, ptrdiff_t rsc, ptrdiff_t csc,
+                                   gk_par par);
+int gk_gemm_packed_b_bf16(gk_workspace *ws, gk_bf16 alpha, const gk_mat_ref *a,
+                          const gk_packed_rhs *packed, gk_bf16 beta, const gk_mat_mut *c,
+                          gk_par par);
+int gk_gemm_packed_b_bf16_unchecked(gk_workspace *ws, gk_bf16 alpha, size_t m, const gk_bf16 *a,
+                                    ptrdiff_t rsa, ptrdiff_t csa, const gk_packed_rhs *packed,
+                                    gk_bf16 beta, gk_bf16 *c, ptrdiff_t rsc, ptrdiff_t csc,
+                                    gk_par par);
+
 /* ----------------------------------------------------------- batched GEMM */
 
 /* gemm_batched::<f32> / _with (src/api/batched.rs:188, :225): element bi uses
@@ -308,6 +340,109 @@ int gk_gemm_batched_bf16_f32out_unchecked(gk_workspace *ws, size_t batch, size_t
                                           ptrdiff_t csb, ptrdiff_t b_bs, float beta, float *c,
                                           ptrdiff_t rsc, ptrdiff_t csc, ptrdiff_t c_bs,
                                           gk_par par);
+
+/* --------------------------------------------- fused bias and activation */
+
+/* Bias (src/api/fused.rs:17-23) / BiasDim (src/kernel/epilogue.rs:205-210):
+ * one value per output row (length m) or per output column (length n),
+ * added after alpha*A*B + beta*C and before the activation. */
+#define GK_BIAS_PER_ROW 0
+#define GK_BIAS_PER_COL 1
+
+/* A checked-tier bias: `data` is a device float* (f32 entries) or gk_bf16*
+ * (bf16 entries), `len` its length in elements, `dim` GK_BIAS_PER_ROW or
+ * GK_BIAS_PER_COL.  A NULL gk_bias* is Option::None. */
+typedef struct gk_bias {
+    const void *data;
+    size_t len;
+    int32_t dim;
+} gk_bias;
+
+/* Semantics of every fused entry (FusedEpi::apply, src/kernel/epilogue.rs:309-330
+ * and :569-596): C <- act(alpha*A*B + beta*C + bias), act = GK_ACT_NONE,
+ * GK_ACT_RELU (v > 0 ? v : 0) or GK_ACT_LEAKY_RELU (max(v,0) + slope*min(v,0));
+ * NaN and -0 map to +0.  f32: bit-identical to the plain GEMM followed by the
+ * same scalar map.  bf16: the map runs in f32 on the accumulator (bias and
+ * slope widened exactly), then one RNE narrowing.  Checked entries add the
+ * reference's bias checks ("gemmkit: PerRow bias length (..) != A.rows (..)",
+ * "... PerCol ... != B.cols", "gemmkit: bias slice overlaps C") and
+ * "gemmkit: LeakyRelu slope must be finite"; with no bias and no activation
+ * they are the plain GEMM.  The unchecked entries take the reference's raw
+ * (bias, bias_dim, has_bias) triple and the activation as (act, slope). */
+
+/* gemm_fused::<f32|bf16> / _with (src/api/fused.rs:61, :81). */
+int gk_gemm_fused_f32(gk_workspace *ws, float alpha, const gk_mat_ref *a, const gk_mat_ref *b,
+                      float beta, const gk_mat_mut *c, const gk_bias *bias, int32_t act,
+                      float slope, gk_par par);
+int gk_gemm_fused_bf16(gk_workspace *ws, gk_bf16 alpha, const gk_mat_ref *a, const gk_mat_ref *b,
+                       gk_bf16 beta, const gk_mat_mut *c, const gk_bias *bias, int32_t act,
+                       gk_bf16 slope, gk_par par);
+/* gemm_fused_unchecked(_with) (src/api/fused.rs:149, :184). */
+int gk_gemm_fused_f32_unchecked(gk_workspace *ws, size_t m, size_t k, size_t n, float alpha,
+                                const float *a, ptrdiff_t rsa, ptrdiff_t csa,
+                                const float *b, ptrdiff_t rsb, ptrdiff_t csb,
+                                float beta, float *c, ptrdiff_t rsc, ptrdiff_t csc,
+                                const float *bias, int32_t bias_dim, uint8_t has_bias,
+                                int32_t act, float slope, gk_par par);
+int gk_gemm_fused_bf16_unchecked(gk_workspace *ws, size_t m, size_t k, size_t n, gk_bf16 alpha,
+                                 const gk_bf16 *a, ptrdiff_t rsa, ptrdiff_t csa,
+                                 const gk_bf16 *b, ptrdiff_t rsb, ptrdiff_t csb,
+                                 gk_bf16 beta, gk_bf16 *c, ptrdiff_t rsc, ptrdiff_t csc,
+                                 const gk_bf16 *bias, int32_t bias_dim, uint8_t has_bias,
+                                 int32_t act, gk_bf16 slope, gk_par par);
+
+/* gemm_batched_fused / _with (src/api/batched.rs:307, :348): one shared bias
+ * vector, sized for a single element, and one activation for every element. */
+int gk_gemm_batched_fused_f32(gk_workspace *ws, size_t batch, float alpha,
+                              const gk_mat_ref *a, ptrdiff_t a_bs,
+                              const gk_mat_ref *b, ptrdiff_t b_bs, float beta,
+                              const gk_mat_mut *c, ptrdiff_t c_bs, const gk_bias *bias,
+                              int32_t act, float slope, gk_par par);
+int gk_gemm_batched_fused_bf16(gk_workspace *ws, size_t batch, gk_bf16 alpha,
+                               const gk_mat_ref *a, ptrdiff_t a_bs,
+                               const gk_mat_ref *b, ptrdiff_t b_bs, gk_bf16 beta,
+                               const gk_mat_mut *c, ptrdiff_t c_bs, const gk_bias *bias,
+                               int32_t act, gk_bf16 slope, gk_par par);
+/* gemm_batched_fused_unchecked(_with) (src/api/batched.rs:459, :523). */
+int gk_gemm_batched_fused_f32_unchecked(gk_workspace *ws, size_t batch, size_t m, size_t k,
+                                        size_t n, float alpha,
+                                        const float *a, ptrdiff_t rsa, ptrdiff_t csa,
+                                        ptrdiff_t a_bs, const float *b, ptrdiff_t rsb,
+                                        ptrdiff_t csb, ptrdiff_t b_bs, float beta, float *c,
+                                        ptrdiff_t rsc, ptrdiff_t csc, ptrdiff_t c_bs,
+                                        const float *bias, int32_t bias_dim, uint8_t has_bias,
+                                        int32_t act, float slope, gk_par par);
+int gk_gemm_batched_fused_bf16_unchecked(gk_workspace *ws, size_t batch, size_t m, size_t k,
+                                         size_t n, gk_bf16 alpha,
+                                         const gk_bf16 *a, ptrdiff_t rsa, ptrdiff_t csa,
+                                         ptrdiff_t a_bs, const gk_bf16 *b, ptrdiff_t rsb,
+                                         ptrdiff_t csb, ptrdiff_t b_bs, gk_bf16 beta, gk_bf16 *c,
+                                         ptrdiff_t rsc, ptrdiff_t csc, ptrdiff_t c_bs,
+                                         const gk_bf16 *bias, int32_t bias_dim,
+                                         uint8_t has_bias, int32_t act, gk_bf16 slope,
+                                         gk_par par);
+
+/* gemm_packed_b_fused / _with (src/api/packed.rs:684, :706): the checks of
+ * gemm_packed_b plus the bias checks; column-major-ish C required. */
+int gk_gemm_packed_b_fused_f32(gk_workspace *ws, float alpha, const gk_mat_ref *a,
+                               const gk_packed_rhs *packed, float beta, const gk_mat_mut *c,
+                               const gk_bias *bias, int32_t act, float slope, gk_par par);
+int gk_gemm_packed_b_fused_bf16(gk_workspace *ws, gk_bf16 alpha, const gk_mat_ref *a,
+                                const gk_packed_rhs *packed, gk_bf16 beta, const gk_mat_mut *c,
+                                const gk_bias *bias, int32_t act, gk_bf16 slope, gk_par par);
+/* gemm_packed_b_fused_unchecked(_with) (src/api/packed.rs:801, :838). */
+int gk_gemm_packed_b_fused_f32_unchecked(gk_workspace *ws, float alpha, size_t m, const float *a,
+                                         ptrdiff_t rsa, ptrdiff_t csa,
+                                         const gk_packed_rhs *packed, float beta, float *c,
+                                         ptrdiff_t rsc, ptrdiff_t csc, const float *bias,
+                                         int32_t bias_dim, uint8_t has_bias, int32_t act,
+                                         float slope, gk_par par);
+int gk_gemm_packed_b_fused_bf16_unchecked(gk_workspace *ws, gk_bf16 alpha, size_t m,
+                                          const gk_bf16 *a, ptrdiff_t rsa, ptrdiff_t csa,
+                                          const gk_packed_rhs *packed, gk_bf16 beta, gk_bf16 *c,
+                                          ptrdiff_t rsc, ptrdiff_t csc, const gk_bf16 *bias,
+                                          int32_t bias_dim, uint8_t has_bias, int32_t act,
+                                          gk_bf16 slope, gk_par par);
 
 #ifdef __cplusplus
 } /* extern "C" */

@@ -98,6 +98,12 @@ def _oracle() -> C.CDLL:
         lib.or_colsum_i32.restype = None
         lib.or_abft_i8.argtypes = [_sz, _sz, _sz, _i8p, _sd, _sd, _i8p, _sd, _sd, _i64p]
         lib.or_abft_i8.restype = None
+        lib.or_fused_map_f32.argtypes = [_sz, _sz, _f32p, _sd, _sd, _f32p, C.c_int, C.c_int,
+                                         C.c_float, _f32p, _sd, _sd]
+        lib.or_fused_map_f32.restype = None
+        lib.or_fused_map_bf16.argtypes = [_sz, _sz, _f32p, _sd, _sd, _u16p, C.c_int, C.c_int,
+                                          C.c_uint16, _u16p, _sd, _sd]
+        lib.or_fused_map_bf16.restype = None
         lib._typed = True
     return lib
 
@@ -240,6 +246,36 @@ def abft_i8(m, k, n, a, rsa, csa, b, rsb, csb) -> np.ndarray:
     out = np.empty(n, np.int64)
     _oracle().or_abft_i8(m, k, n, _ptr(a, _i8p), rsa, csa, _ptr(b, _i8p), rsb, csb,
                          _ptr(out, _i64p))
+    return out
+
+
+def fused_map_f32(v: np.ndarray, bias=None, dim: int = 0, act: int = 0,
+                  slope: float = 0.0) -> np.ndarray:
+    """FusedEpi::apply (f32) over a 2-D float32 array; returns a new array."""
+    v = np.ascontiguousarray(v, np.float32)
+    m, n = v.shape
+    out = np.empty_like(v)
+    bp = None
+    if bias is not None:
+        bias = np.ascontiguousarray(bias, np.float32)
+        bp = _ptr(bias, _f32p)
+    _oracle().or_fused_map_f32(m, n, _ptr(v, _f32p), n, 1, bp, int(dim), int(act),
+                               float(slope), _ptr(out, _f32p), n, 1)
+    return out
+
+
+def fused_map_bf16(v: np.ndarray, bias_bits=None, dim: int = 0, act: int = 0,
+                   slope_bits: int = 0) -> np.ndarray:
+    """The bf16 fused map: f32 values in, bf16 bit patterns out (2-D)."""
+    v = np.ascontiguousarray(v, np.float32)
+    m, n = v.shape
+    out = np.empty((m, n), np.uint16)
+    bp = None
+    if bias_bits is not None:
+        bias_bits = np.ascontiguousarray(bias_bits, np.uint16)
+        bp = _ptr(bias_bits, _u16p)
+    _oracle().or_fused_map_bf16(m, n, _ptr(v, _f32p), n, 1, bp, int(dim), int(act),
+                                int(slope_bits), _ptr(out, _u16p), n, 1)
     return out
 
 

@@ -21,6 +21,12 @@
  *                       hand-checked NaN/inf/ties cases
  *   or_gemm_f64         pinned: README 2x2 KAT, numpy float64 matmul
  *   or_gemv_f64         pinned: numpy float64 matvec
+ *   or_fused_map_f32    pinned: the reference's fused known answers (NaN -> +0
+ *                       under ReLU and LeakyReLU, LeakyReLU(0) with a negative
+ *                       slope -> +0, the degenerate ReLU(0.5*C0 + bias)), and
+ *                       numpy float32 closed forms per activation branch
+ *   or_fused_map_bf16   pinned: or_fused_map_f32 composed with or_bf16_from_f32,
+ *                       plus the bias-widening identity on bf16 inputs
  */
 #include <stdint.h>
 #include <stddef.h>
@@ -322,4 +328,49 @@ OR_API void or_abft_i8(size_t m, size_t k, size_t n,
         for (size_t i = 0; i < m; ++i) s += a[(ptrdiff_t)i * rsa + (ptrdiff_t)p * csa];
         for (size_t j = 0; j < n; ++j) out[j] += s * b[(ptrdiff_t)p * rsb + (ptrdiff_t)j * csb];
     }
+}
+
+/* ----------------------------------------------------------- fused epilogue */
+
+/* FusedEpi::apply for f32 (src/kernel/epilogue.rs:309-330; the tests' scalar
+ * model ref_apply, tests/epilogue/common.rs:74-94) over an m x n matrix of
+ * values v: out[i,j] = act(v[i,j] + bias[ch]) in f32, ch = i (dim 0, PerRow)
+ * or j (dim 1, PerCol), bias == NULL for none; act 0 none, 1 ReLU (v > 0 ? v :
+ * 0), 2 LeakyReLU (hi + slope*lo, hi = v > 0 ? v : 0, lo = v < 0 ? v : 0).
+ * Built with -ffp-contract=off: every operation rounds on its own. */
+static float fused_one_f32(float v, const float *bias, size_t ch, int act, float slope) {
+    if (bias) v = v + bias[ch];
+    if (act == 1) return v > 0.0f ? v : 0.0f;
+    if (act == 2) {
+        float hi = v > 0.0f ? v : 0.0f;
+        float lo = v < 0.0f ? v : 0.0f;
+        return hi + slope * lo;
+    }
+    return v;
+}
+
+OR_API void or_fused_map_f32(size_t m, size_t n, const float *v, ptrdiff_t rv, ptrdiff_t cv,
+                             const float *bias, int dim, int act, float slope, float *out,
+                             ptrdiff_t ro, ptrdiff_t co) {
+    for (size_t i = 0; i < m; ++i)
+        for (size_t j = 0; j < n; ++j)
+            out[(ptrdiff_t)i * ro + (ptrdiff_t)j * co] =
+                fused_one_f32(v[(ptrdiff_t)i * rv + (ptrdiff_t)j * cv], bias, dim ? j : i, act,
+                              slope);
+}
+
+/* The narrow twin (src/kernel/epilogue.rs:569-596): the bf16 bias and slope
+ * widen exactly to f32, the map runs in f32 on the f32 value v, and the result
+ * narrows once with or_bf16_from_f32. */
+OR_API void or_fused_map_bf16(size_t m, size_t n, const float *v, ptrdiff_t rv, ptrdiff_t cv,
+                              const uint16_t *bias, int dim, int act, uint16_t slope,
+                              uint16_t *out, ptrdiff_t ro, ptrdiff_t co) {
+    const float s = or_f32_from_bf16(slope);
+    for (size_t i = 0; i < m; ++i)
+        for (size_t j = 0; j < n; ++j) {
+            float b = bias ? or_f32_from_bf16(bias[dim ? j : i]) : 0.0f;
+            float x = v[(ptrdiff_t)i * rv + (ptrdiff_t)j * cv];
+            out[(ptrdiff_t)i * ro + (ptrdiff_t)j * co] =
+                or_bf16_from_f32(fused_one_f32(x, bias ? &b : NULL, 0, act, s));
+        }
 }

@@ -164,3 +164,78 @@ def test_python_mirror_raises_reference_message():
     with pytest.raises(gk.GemmkitError) as e:
         gk.gemm(1.0, gk.MatRef(a, 2, 5, 5, 1), gk.MatRef(a, 4, 2, 2, 1), 0.0, gk.MatMut(a, 2, 2, 2, 1))
     assert "HIP device" in str(e.value)
+
+
+def bias(data, length, dim):
+    return _lib.BiasC(data, length, dim)
+
+
+# Fused-entry checks (src/api/fused.rs:81-110, src/adapter.rs:130-166; the
+# reference's own cases are tests/epilogue/float.rs:400-470).
+@pytest.mark.parametrize("bs,act,slope,code,msg", [
+    (bias(0x50000, 3, 0), 0, 0.0, -1, "gemmkit: PerRow bias length (3) != A.rows (4)"),
+    (bias(0x50000, 4, 1), 0, 0.0, -1, "gemmkit: PerCol bias length (4) != B.cols (6)"),
+    (None, 2, float("inf"), -4, "gemmkit: LeakyRelu slope must be finite"),
+    (None, 2, float("nan"), -4, "gemmkit: LeakyRelu slope must be finite"),
+    (bias(FAKE_C, 4, 0), 0, 0.0, -3, "gemmkit: bias slice overlaps C"),
+    (bias(FAKE_C + 2 * 23, 6, 1), 1, 0.0, -3, "gemmkit: bias slice overlaps C"),
+    (bias(0x50000, 4, 7), 0, 0.0, -4, "gemmkit: bias dim (7) must be 0 (PerRow) or 1 (PerCol)"),
+    (None, 3, 0.0, -4, "gemmkit: activation (3) must be 0 (none), 1 (Relu) or 2 (LeakyRelu)"),
+])
+def test_checked_fused_validation(bs, act, slope, code, msg):
+    L = _lib.lib()
+    a = ref(FAKE_A, 16, 4, 4, 4, 1)
+    b = ref(FAKE_B, 24, 4, 6, 6, 1)
+    c = mut(FAKE_C, 24, 4, 6, 6, 1)
+    bp = C.byref(bs) if bs is not None else None
+    rc = L.gk_gemm_fused_f32(None, 1.0, C.byref(a), C.byref(b), 0.0, C.byref(c), bp, act, slope, 1)
+    assert (rc, _lib.last_error()) == (code, msg)
+    # The bf16 entry checks the same conditions (bias and C in 2-byte elements:
+    # the overlap cases keep overlapping).
+    slope_bits = 0x7F80 if slope == float("inf") else (0x7FC0 if slope != slope else 0)
+    rc = L.gk_gemm_fused_bf16(None, 0x3F80, C.byref(a), C.byref(b), 0, C.byref(c), bp, act,
+                              slope_bits, 1)
+    assert (rc, _lib.last_error()) == (code, msg)
+
+
+def test_checked_fused_view_checks_come_first():
+    # validate_gemm_views runs before the bias checks (src/api/fused.rs:98-101).
+    L = _lib.lib()
+    a = ref(FAKE_A, 16, 4, 4, 4, 1)
+    b = ref(FAKE_B, 24, 3, 6, 6, 1)
+    c = mut(FAKE_C, 24, 4, 6, 6, 1)
+    bs = bias(0x50000, 3, 0)
+    rc = L.gk_gemm_fused_f32(None, 1.0, C.byref(a), C.byref(b), 0.0, C.byref(c), C.byref(bs),
+                             0, 0.0, 1)
+    assert rc == -1 and _lib.last_error() == "gemmkit: A.cols (4) != B.rows (3)"
+
+
+def test_checked_batched_fused_validation():
+    L = _lib.lib()
+    a = ref(FAKE_A, 1000, 10, 10, 10, 1)
+    b = ref(FAKE_B, 1000, 10, 10, 10, 1)
+    c = mut(FAKE_C, 1000, 10, 10, 10, 1)
+    # The bias is one shared vector sized for a single element.
+    bs = bias(0x90000, 30, 0)
+    rc = L.gk_gemm_batched_fused_f32(None, 3, 1.0, C.byref(a), 100, C.byref(b), 100, 0.0,
+                                     C.byref(c), 100, C.byref(bs), 0, 0.0, 1)
+    assert rc == -1 and _lib.last_error() == "gemmkit: PerRow bias length (30) != A.rows (10)"
+    bs = bias(FAKE_C + 4 * 999, 10, 1)
+    rc = L.gk_gemm_batched_fused_f32(None, 3, 1.0, C.byref(a), 100, C.byref(b), 100, 0.0,
+                                     C.byref(c), 100, C.byref(bs), 0, 0.0, 1)
+    assert rc == -3 and _lib.last_error() == "gemmkit: bias slice overlaps C"
+    # batch == 0 returns before any check.
+    rc = L.gk_gemm_batched_fused_f32(None, 0, 1.0, C.byref(a), -5, C.byref(b), 100, 0.0,
+                                     C.byref(c), 100, C.byref(bs), 0, 0.0, 1)
+    assert rc == 0
+
+
+def test_packed_fused_null_handle():
+    L = _lib.lib()
+    a = ref(FAKE_A, 16, 4, 4, 4, 1)
+    c = mut(FAKE_C, 24, 4, 6, 1, 4)
+    rc = L.gk_gemm_packed_b_fused_f32(None, 1.0, C.byref(a), None, 0.0, C.byref(c), None, 1,
+                                      0.0, 1)
+    assert rc == -4 and _lib.last_error() == "gemmkit: null argument"
+    rc = L.gk_gemm_packed_b_f32_unchecked(None, 1.0, 4, FAKE_A, 4, 1, None, 0.0, FAKE_C, 1, 4, 1)
+    assert rc == -4 and _lib.last_error() == "gemmkit: null packed RHS"

@@ -188,6 +188,81 @@ def test_bf16_nan_rule():
         assert oracle.bf16_bits(f)[0] == ((bits >> 16) | 0x40)
 
 
+# ------------------------------------------------------------ fused epilogue
+
+def _bits(x):
+    return np.asarray(x, np.float32).view(np.uint32)
+
+
+def test_fused_map_reference_kats():
+    # tests/epilogue/float.rs:274-358: a NaN value maps to +0 under ReLU and
+    # LeakyReLU(0.25); a zero product under LeakyReLU(-0.5) is +0, not -0.
+    nan = np.full((3, 5), np.nan, np.float32)
+    assert (_bits(oracle.fused_map_f32(nan, act=1)) == 0).all()
+    assert (_bits(oracle.fused_map_f32(nan, act=2, slope=0.25)) == 0).all()
+    zeros = np.array([[0.0, -0.0, 0.0]], np.float32)
+    assert (_bits(oracle.fused_map_f32(zeros, act=2, slope=-0.5)) == 0).all()
+    assert (_bits(oracle.fused_map_f32(zeros, act=1)) == 0).all()
+    # tests/epilogue/float.rs:361-395: the degenerate ReLU(0.5*C0 + bias[i]),
+    # checked here against numpy's own float32 ops: the f32 sum of two f32
+    # values equals the f64 sum rounded to f32, and max(x, 0) + 0 is ReLU with
+    # -0 sent to +0.
+    c0 = oracle.rng_unit(0xDE6E, 20 * 24).astype(np.float32).reshape(20, 24)
+    bias = oracle.rng_unit(7, 20).astype(np.float32)
+    base = np.float32(0.5) * c0
+    got = oracle.fused_map_f32(base, bias, 0, 1)
+    want = np.maximum((base.astype(np.float64) + bias[:, None]).astype(np.float32),
+                      np.float32(0)) + np.float32(0)
+    assert np.array_equal(_bits(got), _bits(want))
+
+
+def test_fused_map_closed_forms():
+    x = np.concatenate([oracle.rng_normal(3, 4000).astype(np.float32) *
+                        np.float32(10.0) ** np.arange(-4, 4).repeat(500).astype(np.float32),
+                        np.array([0.0, -0.0, np.inf, -np.inf, 1e-45, -1e-45, 3e38, -3e38],
+                                 np.float32)]).reshape(1, -1)
+    m, n = 3, x.shape[1]
+    v = np.repeat(x, m, axis=0)
+    brow = np.array([0.0, 1.5, -2.25], np.float32)
+    bcol = oracle.rng_unit(9, n).astype(np.float32)
+    for bias, dim in ((None, 0), (brow, 0), (bcol, 1)):
+        if bias is None:
+            y = v
+        else:
+            b = bias[:, None] if dim == 0 else bias[None, :]
+            with np.errstate(invalid="ignore", over="ignore"):
+                y = (v.astype(np.float64) + b).astype(np.float32)
+        # no activation: the bias add alone
+        assert np.array_equal(_bits(oracle.fused_map_f32(v, bias, dim, 0)), _bits(y))
+        # ReLU
+        with np.errstate(invalid="ignore"):
+            want = np.where(np.isnan(y), np.float32(0), np.maximum(y, np.float32(0))) + np.float32(0)
+        assert np.array_equal(_bits(oracle.fused_map_f32(v, bias, dim, 1)), _bits(want))
+        # LeakyReLU: y for y > 0, the f32 product slope*y (then +0) for y < 0, +0
+        # otherwise (zeros and NaN).  1e-45 * 0.25 underflows to -0 for a
+        # negative input: a fused multiply-add would keep -0, the map gives +0.
+        for slope in (0.1, 0.25, -0.5, 3.0):
+            s = np.float32(slope)
+            with np.errstate(invalid="ignore", over="ignore"):
+                neg = (s * y) + np.float32(0)
+                want = np.where(y > 0, y, np.where(y < 0, neg, np.float32(0))).astype(np.float32)
+            got = oracle.fused_map_f32(v, bias, dim, 2, slope)
+            assert np.array_equal(_bits(got), _bits(want)), (slope, dim)
+
+
+def test_fused_map_bf16_widens_and_narrows_once():
+    import torch
+    v = (oracle.rng_normal(11, 6 * 50) * 4).astype(np.float32).reshape(6, 50)
+    bias = oracle.bf16_bits(oracle.rng_unit(12, 50).astype(np.float32))
+    slope = int(oracle.bf16_bits(np.array([0.1], np.float32))[0])
+    for act in (0, 1, 2):
+        got = oracle.fused_map_bf16(v, bias, 1, act, slope)
+        f32 = oracle.fused_map_f32(v, oracle.bf16_to_f32(bias), 1, act,
+                                   float(oracle.bf16_to_f32(np.array([slope]))[0]))
+        want = torch.from_numpy(f32).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+        assert np.array_equal(got, want)
+
+
 # ----------------------------------------------------------------- f64 GEMM
 
 def test_readme_kat_f64():
