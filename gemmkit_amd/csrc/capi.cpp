@@ -376,6 +376,28 @@ Tile pick_tile(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind kind
     return bt;
 }
 
+// Split K: when the 64 x 64 tiles of one product leave most CUs idle and K is
+// long, each tile's K is cut into ranges of at least kSplitMinBytes, enough
+// of them for about two workgroups per CU.  The choice depends on the
+// element shape only (never on the batch count), so a batched element equals
+// the standalone product bit for bit.  GEMMKIT_HIP_SPLITK=0 turns it off.
+constexpr int64_t kSplitMinBytes = 256;
+constexpr int64_t kMaxSplits = 32;
+
+int choose_splits(int64_t M, int64_t N, int64_t k, size_t esz) {
+    const char *s = getenv("GEMMKIT_HIP_SPLITK");
+    if (s && !strcmp(s, "0")) return 1;
+    bool forced;
+    (void)env_tile(&forced);
+    if (forced) return 1;
+    const int64_t kbytes = k * (int64_t)esz;
+    const int64_t t64 = ((M + 63) / 64) * ((N + 63) / 64);
+    const int64_t cus = g_num_cus > 0 ? g_num_cus : 256;
+    if (2 * t64 > cus || kbytes < 2 * kSplitMinBytes) return 1;
+    return (int)std::min<int64_t>(std::min<int64_t>(2 * cus / t64, kbytes / kSplitMinBytes),
+                                  kMaxSplits);
+}
+
 // The shared core: C = epi(A*B) for every batch element.  `ep` comes in the
 // user frame (rsc/csc of the user's C, axis 0 = per user row); m, k, n >= 1.
 int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t k, int64_t n,
@@ -407,43 +429,61 @@ int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t
     gk_workspace *ws = resolve_ws(ws_in);
     const bool a_ok = canonical(A, M, k, esz, batch);
     const bool b_ok = canonical(Bt, N, k, esz, batch);
-    if (!a_ok || !b_ok) {
-        size_t need = (a_ok ? 0 : pack_bytes(in, M, k, batch, A)) +
-                      (b_ok ? 0 : pack_bytes(in, N, k, batch, Bt));
+
+    // Route.  The matrix-core kernels address a tile's rows with 32-bit
+    // offsets from its first row: 256 row strides plus a row must stay below
+    // 2 GiB (row strides as they will be after any pack).
+    const int64_t pld = round_up64(std::max<int64_t>(k, 1), 16 / (int64_t)esz);
+    const int64_t a_rs = a_ok ? A.rs : pld, b_rs = b_ok ? Bt.rs : pld;
+    const bool k_fits = k * (int64_t)esz <= kMaxTileRowBytes;
+    const bool offsets_fit = std::max(a_rs, b_rs) * (int64_t)esz <= kMaxTileRowBytes && k_fits;
+    const int64_t short_side = std::min(M, N);
+    // Skinny products: the short side's rows are the vectors.  One vector
+    // streams best with the wavefront GEMV (a whole 1 KiB row segment per
+    // load, no cross-wave exchange); 2..16 vectors go to the matrix-core
+    // skinny kernel, which stages the vectors from any strides itself (only
+    // the long operand must be k-contiguous).
+    const bool vec_is_a = M <= N;
+    const bool skinny_ok = short_side >= 2 && short_side <= 16 && skinny_enabled() && k_fits &&
+                           (vec_is_a ? b_rs : a_rs) * (int64_t)esz <= kMaxTileRowBytes &&
+                           skinny_lds_bytes(in, k, (int)short_side) <= kSkinnyLdsMax;
+    const bool vector_route = skinny_ok || short_side <= 8;
+    const bool pack_a = !a_ok && !(skinny_ok && vec_is_a);
+    const bool pack_b = !b_ok && !(skinny_ok && !vec_is_a);
+    int splits = vector_route ? 1 : choose_splits(M, N, k, esz);
+    // K ranges of whole 64-byte stages; rounding up may leave fewer ranges,
+    // every one of them non-empty.
+    const int64_t kchunk = splits > 1 ? round_up64((k + splits - 1) / splits, 64 / (int64_t)esz) : k;
+    splits = (int)((k + kchunk - 1) / kchunk);
+    const size_t part_bytes =
+        splits > 1 ? (size_t)round_up64((int64_t)batch * splits * M * N * 4, 256) : 0;
+
+    uint8_t *part = nullptr;
+    if (pack_a || pack_b || part_bytes) {
+        const size_t a_bytes = pack_a ? pack_bytes(in, M, k, batch, A) : 0;
+        const size_t b_bytes = pack_b ? pack_bytes(in, N, k, batch, Bt) : 0;
         void *base = nullptr;
-        int r = ws_reserve(ws, need, &base);
+        int r = ws_reserve(ws, a_bytes + b_bytes + part_bytes, &base);
         if (r) return r;
         uint8_t *dst = (uint8_t *)base;
-        if (!a_ok) {
-            size_t used = pack_bytes(in, M, k, batch, A);
-            if ((r = materialize(in, A, M, k, batch, dst, &A))) return r;
-            dst += used;
-        }
-        if (!b_ok && (r = materialize(in, Bt, N, k, batch, dst, &Bt))) return r;
+        if (pack_a && (r = materialize(in, A, M, k, batch, dst, &A))) return r;
+        if (pack_b && (r = materialize(in, Bt, N, k, batch, dst + a_bytes, &Bt))) return r;
+        part = dst + a_bytes + b_bytes;
     }
 
     hipError_t e;
-    const int64_t short_side = std::min(M, N);
-    // The matrix-core kernels address a tile's rows with 32-bit offsets from
-    // its first row: 256 row strides plus a row must stay below 2 GiB.
-    const bool offsets_fit = std::max(A.rs, Bt.rs) * (int64_t)esz <= kMaxTileRowBytes &&
-                             k * (int64_t)esz <= kMaxTileRowBytes;
-    // One vector streams best with the wavefront GEMV (a whole 1 KiB row
-    // segment per load, no cross-wave exchange); 2..16 vectors go to the
-    // matrix-core kernel.
-    const bool skinny_ok = short_side >= 2 && short_side <= 16 && skinny_enabled() && offsets_fit &&
-                           skinny_lds_bytes(in, k, (int)short_side) <= kSkinnyLdsMax;
-    if (skinny_ok || short_side <= 8) {
+    if (vector_route) {
         // Skinny route: the short side's rows are the vectors, streamed
         // against the long side's rows (matrix-core kernel up to 16 vectors
         // when the vectors fit in LDS, else the wavefront-reduction GEMV).
-        const bool vec_is_a = M <= N;
         GemvArgs g{};
         EpiParams eg = ep;
         if (vec_is_a) {
-            g.mat = Bt.p; g.ld = Bt.rs; g.vec = A.p; g.vld = A.rs; g.R = (int32_t)N; g.nvec = (int32_t)M;
+            g.mat = Bt.p; g.ld = Bt.rs; g.vec = A.p; g.vld = A.rs; g.vks = A.ks;
+            g.R = (int32_t)N; g.nvec = (int32_t)M;
         } else {
-            g.mat = A.p; g.ld = A.rs; g.vec = Bt.p; g.vld = Bt.rs; g.R = (int32_t)M; g.nvec = (int32_t)N;
+            g.mat = A.p; g.ld = A.rs; g.vec = Bt.p; g.vld = Bt.rs; g.vks = Bt.ks;
+            g.R = (int32_t)M; g.nvec = (int32_t)N;
             std::swap(eg.rsc, eg.csc);
             eg.axis ^= 1;
         }
@@ -486,6 +526,28 @@ int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t
     args.N = (int32_t)N;
     args.K = (int32_t)k;
     args.batch = (int32_t)batch;
+    args.splits = 1;
+    if (splits > 1) {
+        // Partial sums of each K range into their own slab (i32 for i8
+        // inputs, f32 otherwise), then one pass sums the slabs in range order
+        // and applies the call's epilogue.
+        args.splits = splits;
+        args.kchunk = (int32_t)kchunk;
+        EpiParams pe{};
+        pe.kind = in == InType::I8 ? EpiKind::I32 : EpiKind::F32;
+        pe.alpha_i = 1;
+        pe.alpha_f = 1.0f;
+        pe.c = part;
+        pe.rsc = N;
+        pe.csc = 1;
+        pe.bsc = M * N;
+        pe.vec4 = N % 4 == 0;
+        e = launch_mma(in, Tile::T64x64, args, pe, tl_stream);
+        if (e != hipSuccess) return hip_fail(e, "mfma launch");
+        e = launch_split_reduce(in, part, splits, M, N, batch, ep, tl_stream);
+        if (e != hipSuccess) return hip_fail(e, "split reduce launch");
+        return finish("mfma gemm (split K)");
+    }
     e = launch_mma(in, pick_tile(M, N, batch, k * (int64_t)esz, ep.kind), args, ep, tl_stream);
     if (e != hipSuccess) return hip_fail(e, "mfma launch");
     return finish("mfma gemm");

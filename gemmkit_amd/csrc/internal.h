@@ -61,6 +61,10 @@ struct MmaArgs {
     int64_t bsa, bsb;      // batch strides in elements
     int32_t M, N, K;       // K in elements
     int32_t batch;
+    // Split K (1 = off): K range r = [r*kchunk, min(K, (r+1)*kchunk)) of batch
+    // element b writes its partial sums to output slab b*splits + r; kchunk
+    // is a multiple of 64 bytes of K.
+    int32_t splits, kchunk;
 };
 
 // Tile shapes instantiated in mfma_{i8,bf16,f32}.hip.
@@ -83,8 +87,8 @@ hipError_t launch_mma(InType in, Tile tile, const MmaArgs &args, const EpiParams
 struct GemvArgs {
     const void *mat;       // R x K, k-contiguous rows, ld elements apart
     int64_t ld;
-    const void *vec;       // nvec x K, k-contiguous, vld apart
-    int64_t vld;
+    const void *vec;       // nvec x K: element (j, p) at vec + j*vld + p*vks
+    int64_t vld, vks;      // vks == 1 (k-contiguous) except on the skinny route
     int32_t R, K, nvec;
     int32_t cus;           // compute units of the device (persistent grid size)
     // Output element (vector j, matrix row r) is stored as the epilogue's
@@ -93,8 +97,8 @@ struct GemvArgs {
 hipError_t launch_gemv(InType in, const GemvArgs &g, const EpiParams &ep, hipStream_t stream);
 
 // Matrix-core skinny route (1..16 vectors): the vectors are staged in LDS,
-// which must hold skinny_lds_bytes() <= kSkinnyLdsMax.
-constexpr int64_t kSkinnyLdsMax = 64 * 1024;
+// which must hold skinny_lds_bytes() <= kSkinnyLdsMax (a CU has 160 KiB).
+constexpr int64_t kSkinnyLdsMax = 128 * 1024;
 int64_t skinny_lds_bytes(InType in, int64_t K, int nvec);
 hipError_t launch_skinny(InType in, const GemvArgs &g, const EpiParams &ep, hipStream_t stream);
 
@@ -111,6 +115,12 @@ hipError_t launch_scale_c(EpiKind kind, void *c, int64_t m, int64_t n, int64_t r
 
 // k == 0 requant fill (requant_degenerate, src/dispatch/int.rs:735-752).
 hipError_t launch_requant_fill(const EpiParams &ep, int64_t m, int64_t n, hipStream_t stream);
+
+// Split-K reduction: C = epi(sum over r of partial slab b*splits + r), the
+// slabs (M x N, row-major, i32 for i8 inputs, f32 otherwise) summed in r
+// order; `ep` in the kernel frame, batch element b at ep.bsc.
+hipError_t launch_split_reduce(InType in, const void *part, int splits, int64_t M, int64_t N,
+                               int64_t batch, const EpiParams &ep, hipStream_t stream);
 
 // Fused degenerate map C <- act(beta*C + bias) when the A*B term vanishes
 // (fused_degenerate_float, src/dispatch/float.rs:739-758; fused_degenerate_mixed,

@@ -176,7 +176,7 @@ constexpr int waves_per_simd() {
     return wgs * WM * WN / 4 > 1 ? wgs * WM * WN / 4 : 1;
 }
 
-template <InType T, EpiKind E, int BM, int BN, int WM, int WN, int BK, int NS>
+template <InType T, EpiKind E, int BM, int BN, int WM, int WN, int BK, int NS, bool SPLIT>
 __global__ __launch_bounds__(WM * WN * 64)
 __attribute__((amdgpu_waves_per_eu(waves_per_simd<BM, BN, WM, WN, BK, NS>(),
                                    waves_per_simd<BM, BN, WM, WN, BK, NS>())))
@@ -211,13 +211,23 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     int tmi, tni;
     tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tmi, tni);
     const int m0 = tmi * BM, n0 = tni * BN;
+    // Output slab z.  SPLIT: z = batch element * splits + K range, and each
+    // range's partial sums go to a slab of their own (the epilogue's batch
+    // stride), to be reduced in range order afterwards.  The unsplit kernels
+    // are separate instantiations, so their code is untouched by this.
     const int64_t z = blockIdx.z;
+    int64_t zb = z, k0 = 0, kel = args.K;
+    if constexpr (SPLIT) {
+        zb = z / args.splits;
+        k0 = (z % args.splits) * (int64_t)args.kchunk;
+        kel = args.K - k0 < args.kchunk ? args.K - k0 : args.kchunk;
+    }
 
     const int esz = (T == InType::I8) ? 1 : (T == InType::BF16 ? 2 : 4);
-    const int64_t kbytes = (int64_t)args.K * esz;
+    const int64_t kbytes = kel * esz;
     const int64_t lda_b = args.lda * esz, ldb_b = args.ldb * esz;
-    const uint8_t *A = (const uint8_t *)args.a + z * args.bsa * esz;
-    const uint8_t *B = (const uint8_t *)args.b + z * args.bsb * esz;
+    const uint8_t *A = (const uint8_t *)args.a + (zb * args.bsa + k0) * esz;
+    const uint8_t *B = (const uint8_t *)args.b + (zb * args.bsb + k0) * esz;
     const int KT = (int)((kbytes + BK - 1) / BK);
     const bool k_whole = (kbytes % BK) == 0;
 
@@ -485,18 +495,26 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     }
 }
 
-template <InType T, EpiKind E, int BM, int BN, int WM, int WN, int NS>
+template <InType T, EpiKind E, int BM, int BN, int WM, int WN, int NS, bool SPLIT = false>
 static hipError_t launch_one(const MmaArgs &args, const EpiParams &ep, hipStream_t stream) {
     int tiles = ((args.M + BM - 1) / BM) * ((args.N + BN - 1) / BN);
-    dim3 grid(tiles, 1, args.batch);
-    hipLaunchKernelGGL((mma_kernel<T, E, BM, BN, WM, WN, 64, NS>), grid, dim3(WM * WN * 64), 0,
-                       stream, args, ep);
+    dim3 grid(tiles, 1, args.batch * (SPLIT ? args.splits : 1));
+    hipLaunchKernelGGL((mma_kernel<T, E, BM, BN, WM, WN, 64, NS, SPLIT>), grid,
+                       dim3(WM * WN * 64), 0, stream, args, ep);
     return hipGetLastError();
 }
 
+// A split K runs on the 64 x 64 tile only (the host's choice); the partial
+// products are always the native accumulator type.
 template <InType T, EpiKind E>
 static hipError_t launch_tile(Tile tile, const MmaArgs &args, const EpiParams &ep,
                               hipStream_t stream) {
+    if (args.splits > 1) {
+        if constexpr (E == Mma<T>::native) {
+            if (tile == Tile::T64x64) return launch_one<T, E, 64, 64, 2, 2, 4, true>(args, ep, stream);
+        }
+        return hipErrorInvalidValue;
+    }
     switch (tile) {
     case Tile::T256x256: return launch_one<T, E, 256, 256, 2, 2, 4>(args, ep, stream);
     case Tile::T256x256w8: return launch_one<T, E, 256, 256, 2, 4, 4>(args, ep, stream);

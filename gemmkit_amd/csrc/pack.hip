@@ -12,6 +12,10 @@
 //                    src/dispatch/int.rs:735-752).
 //   fused_fill       C <- act(beta*C + bias) when the A*B term of a fused
 //                    call vanishes (src/dispatch/float.rs:661-680).
+//   split_reduce     sums the partial products of a split-K matrix-core launch
+//                    and applies the call's epilogue.
+#include <type_traits>
+
 #include "epilogue.h"
 
 namespace gk {
@@ -25,17 +29,27 @@ __global__ __launch_bounds__(256) void pack_kernel(const T *__restrict__ src, in
     const int64_t p0 = (int64_t)blockIdx.x * 64;
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // 64 x 4
     // Read: let consecutive threads walk the operand's faster-moving index.
+    // All 16 loads of a thread are issued before any is used (one memory
+    // round trip per tile, not sixteen).
     const bool k_fast = (cs < 0 ? -cs : cs) <= (rs < 0 ? -rs : rs);
-    for (int y = ty; y < 64; y += 4) {
+    T v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int y = ty + 4 * i;
         int64_t r, p;
         if (k_fast) { r = r0 + y; p = p0 + tx; } else { r = r0 + tx; p = p0 + y; }
-        T v = T(0);
-        if (r < rows && p < K) v = src[r * rs + p * cs];
-        if (k_fast) tile[y][tx] = v; else tile[tx][y] = v;
+        v[i] = (r < rows && p < K) ? src[r * rs + p * cs] : T(0);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int y = ty + 4 * i;
+        if (k_fast) tile[y][tx] = v[i]; else tile[tx][y] = v[i];
     }
     __syncthreads();
     // Write: consecutive threads write consecutive k; columns [K, ld) get zeros.
-    for (int y = ty; y < 64; y += 4) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int y = ty + 4 * i;
         int64_t r = r0 + y, p = p0 + tx;
         if (r < rows && p < ld) dst[r * ld + p] = (p < K) ? tile[y][tx] : T(0);
     }
@@ -103,6 +117,81 @@ hipError_t launch_requant_fill(const EpiParams &ep, int64_t m, int64_t n, hipStr
     if (m == 0 || n == 0) return hipSuccess;
     dim3 grid((unsigned)((m * n + 255) / 256));
     hipLaunchKernelGGL(requant_fill_kernel, grid, dim3(256), 0, stream, ep, m, n);
+    return hipGetLastError();
+}
+
+// Split-K reduction: one thread per 4 consecutive output elements of one
+// batch element (blockIdx.y) when N % 4 == 0 (16-byte partial loads), else
+// one per element.  The partial slabs are summed in K-range order (wrapping
+// for i32), eight slabs' loads in flight at a time, then stored through the
+// call's epilogue.
+template <EpiKind E, typename A, int W>
+__global__ __launch_bounds__(256) void split_reduce_kernel(const A *__restrict__ part, int splits,
+                                                           int64_t M, int64_t N,
+                                                           const EpiParams ep) {
+    typedef A vec_t __attribute__((ext_vector_type(W)));
+    const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * W;
+    const int64_t z = blockIdx.y;
+    const int64_t slab = M * N;
+    if (idx >= slab) return;
+    const A *p = part + z * splits * slab + idx;
+    vec_t acc = *(const vec_t *)p;
+    for (int r0 = 1; r0 < splits; r0 += 8) {
+        vec_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (r0 + u < splits) v[u] = *(const vec_t *)(p + (r0 + u) * slab);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (r0 + u < splits) {
+                if constexpr (std::is_integral<A>::value) {
+#pragma unroll
+                    for (int e = 0; e < W; ++e) acc[e] = (A)((uint32_t)acc[e] + (uint32_t)v[u][e]);
+                } else {
+                    acc = acc + v[u];
+                }
+            }
+        }
+    }
+    const int row = (int)(idx / N), col = (int)(idx % N);
+#pragma unroll
+    for (int e = 0; e < W; ++e) Store<E>::apply(ep, z, row, col + e, acc[e]);
+}
+
+template <EpiKind E, typename A>
+static void split_reduce_go(const A *p, int splits, int64_t M, int64_t N, int64_t batch,
+                            const EpiParams &ep, hipStream_t stream) {
+    if (N % 4 == 0) {
+        dim3 grid((unsigned)((M * N / 4 + 255) / 256), (unsigned)batch);
+        hipLaunchKernelGGL((split_reduce_kernel<E, A, 4>), grid, dim3(256), 0, stream, p, splits,
+                           M, N, ep);
+    } else {
+        dim3 grid((unsigned)((M * N + 255) / 256), (unsigned)batch);
+        hipLaunchKernelGGL((split_reduce_kernel<E, A, 1>), grid, dim3(256), 0, stream, p, splits,
+                           M, N, ep);
+    }
+}
+
+hipError_t launch_split_reduce(InType in, const void *part, int splits, int64_t M, int64_t N,
+                               int64_t batch, const EpiParams &ep, hipStream_t stream) {
+    if (M == 0 || N == 0 || batch == 0) return hipSuccess;
+    if (in == InType::I8) {
+        const int32_t *p = (const int32_t *)part;
+        if (ep.kind == EpiKind::I32)
+            split_reduce_go<EpiKind::I32>(p, splits, M, N, batch, ep, stream);
+        else if (ep.kind == EpiKind::Q8)
+            split_reduce_go<EpiKind::Q8>(p, splits, M, N, batch, ep, stream);
+        else
+            return hipErrorInvalidValue;
+    } else {
+        const float *p = (const float *)part;
+        if (ep.kind == EpiKind::F32)
+            split_reduce_go<EpiKind::F32>(p, splits, M, N, batch, ep, stream);
+        else if (ep.kind == EpiKind::BF16)
+            split_reduce_go<EpiKind::BF16>(p, splits, M, N, batch, ep, stream);
+        else
+            return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -22,10 +22,16 @@
 // distinct banks); the matrix goes global -> VGPRs through a buffer resource
 // (rows past R and bytes past K read as zeros).
 //
-// Work item: 32 matrix rows (four 8-row blocks) x all of K.  The 4 waves of a
-// workgroup split K into 4 contiguous ranges; each keeps 4 k steps x 4 blocks
-// (16 KiB) of loads in flight behind its MFMAs, and the four partial sums are
-// added through LDS, in wave order, before the epilogue.
+// Work item: BLK 8-row blocks (32 rows, or 8 when there are too few rows to
+// give every CU an item) x all of K.  The 4 waves of a workgroup split K into
+// 4 contiguous ranges; each keeps 4 k steps x BLK blocks of loads in flight
+// behind its MFMAs, and the four partial sums are added through LDS, in wave
+// order, before the epilogue.
+// The vectors may have any strides: k-contiguous, 16-byte aligned rows are
+// staged as 16-byte chunks, anything else element by element (so a strided
+// activation needs no separate pack launch).
+#include <type_traits>
+
 #include "epilogue.h"
 
 namespace gk {
@@ -72,8 +78,7 @@ struct Mma16<InType::F32> {
 
 constexpr int kSkThreads = 256;
 constexpr int kSkWaves = 4;
-constexpr int kSkBlocks = 4;               // 8-row blocks per work item
-constexpr int kSkRows = 8 * kSkBlocks;     // matrix rows per work item
+constexpr int kSkBlocks = 4;               // 8-row blocks per work item (at most)
 constexpr int kSkStep = 128;               // k bytes per step (one load per block)
 constexpr int kSkPF = 4;                   // k steps per load batch
 constexpr int kSkCombine = kSkWaves * kSkBlocks * 2 * 64 * 4;  // partial-sum exchange bytes
@@ -92,8 +97,9 @@ __device__ __forceinline__ v4i_s load16(const uint8_t *base, uint32_t num, uint3
     return __builtin_bit_cast(v4i_s, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
-template <InType T, EpiKind E>
+template <InType T, EpiKind E, int BLK>
 __global__ __launch_bounds__(kSkThreads) void skinny_mfma(const GemvArgs g, const EpiParams ep) {
+    constexpr int kSkRows = 8 * BLK;  // matrix rows per work item
     using Mm = Mma16<T>;
     using acc_t = typename Mm::acc_t;
     using val_t = typename Mm::val_t;
@@ -129,10 +135,10 @@ __global__ __launch_bounds__(kSkThreads) void skinny_mfma(const GemvArgs g, cons
     const int my_items = (int)blockIdx.x < items ? (items - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
     const int nbw = ks1 > ks0 ? (ks1 - ks0 + kSkPF - 1) / kSkPF : 1;
     const int total = my_items * nbw;
-    uint32_t off[kSkBlocks];
+    uint32_t off[BLK];
 #pragma unroll
-    for (int b = 0; b < kSkBlocks; ++b) off[b] = (uint32_t)((8 * b + (li >> 1)) * ld_b + 16 * chunk);
-    auto issue = [&](int t, v4i_s (&m)[kSkPF][kSkBlocks]) {
+    for (int b = 0; b < BLK; ++b) off[b] = (uint32_t)((8 * b + (li >> 1)) * ld_b + 16 * chunk);
+    auto issue = [&](int t, v4i_s (&m)[kSkPF][BLK]) {
         const int r0 = ((int)blockIdx.x + (t / nbw) * (int)gridDim.x) * kSkRows;
         const int s0 = ks0 + (t % nbw) * kSkPF;
         const uint8_t *base = mat + (int64_t)r0 * ld_b;
@@ -146,43 +152,109 @@ __global__ __launch_bounds__(kSkThreads) void skinny_mfma(const GemvArgs g, cons
             const int s = s0 + p;
             const bool in = s < ks1 && (int64_t)s * kSkStep + 16 * chunk < kb;
 #pragma unroll
-            for (int b = 0; b < kSkBlocks; ++b)
+            for (int b = 0; b < BLK; ++b)
                 m[p][b] = load16(base, num, in ? off[b] + (uint32_t)s * kSkStep : kSkOut);
         }
     };
-    v4i_s buf0[kSkPF][kSkBlocks], buf1[kSkPF][kSkBlocks];
+    v4i_s buf0[kSkPF][BLK], buf1[kSkPF][BLK];
     if (total > 0) issue(0, buf0);  // in flight while the vectors are staged
 
-    // Stage the vectors: nvec rows of kb bytes, 8 chunks per thread in flight
-    // at a time (one L2 round trip for up to 32 KiB).
+    // Stage the vectors: nvec rows of kb bytes (zeros past K), 8 chunks or
+    // elements per thread in flight at a time (one L2 round trip for up to
+    // 32 KiB).
     const uint8_t *vec = (const uint8_t *)g.vec;
-    const int64_t vld_b = g.vld * esz, cpr = kb / 16, nchunks = nvec * cpr;
-    for (int64_t c0 = tid; c0 < nchunks; c0 += kSkThreads * 8) {
-        v4i_s tmp[8];
+    const int64_t vld_b = g.vld * esz;
+    if (g.vks == 1 && g.K * esz % 16 == 0 && vld_b % 16 == 0 && (uintptr_t)vec % 16 == 0) {
+        const int64_t cpr = kb / 16, nchunks = nvec * cpr;
+        for (int64_t c0 = tid; c0 < nchunks; c0 += kSkThreads * 8) {
+            v4i_s tmp[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int64_t c = c0 + (int64_t)u * kSkThreads;
-            tmp[u] = c < nchunks ? *(const v4i_s *)(vec + (c / cpr) * vld_b + (c % cpr) * 16)
-                                 : v4i_s{0, 0, 0, 0};
+            for (int u = 0; u < 8; ++u) {
+                const int64_t c = c0 + (int64_t)u * kSkThreads;
+                tmp[u] = c < nchunks ? *(const v4i_s *)(vec + (c / cpr) * vld_b + (c % cpr) * 16)
+                                     : v4i_s{0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int64_t c = c0 + (int64_t)u * kSkThreads;
+                if (c < nchunks) *(v4i_s *)(sh + (c / cpr) * xs + (c % cpr) * 16) = tmp[u];
+            }
         }
+    } else if (g.vld == 1 && g.vks >= nvec && (uintptr_t)vec % 4 == 0 &&
+               (int64_t)(g.K - 1) * g.vks + nvec <= 0xFFFFFFFFll) {
+        // Column-major vectors (element (j, p) at p*vks + j): the span they
+        // cover is read as aligned 4-byte words, 8 per thread in flight, and
+        // each element is scattered to its vector's row.  A word never
+        // straddles a page, so the bytes a last partial word reads past the
+        // span are mapped; they are discarded.
+        using elem_t = typename std::conditional<esz == 1, uint8_t,
+                         typename std::conditional<esz == 2, uint16_t, uint32_t>::type>::type;
+        constexpr int EPW = 4 / esz;  // elements per word
+        const uint32_t vks = (uint32_t)g.vks;
+        // idx / vks as a multiply-high (Granlund-Montgomery, exact for every
+        // 32-bit idx): l = ceil(log2 vks), magic = 2^32 (2^l - vks) / vks + 1.
+        const int dl = 32 - __builtin_clz(vks - 1);
+        const uint32_t magic = (uint32_t)(((1ull << 32) * ((1ull << dl) - vks)) / vks + 1);
+        const int64_t span = ((int64_t)(g.K - 1) * vks + nvec) * esz;
+        const int64_t nw = (span + 3) / 4;
+        const uint32_t *vw = (const uint32_t *)vec;
+        for (int64_t w0 = tid; w0 < nw; w0 += kSkThreads * 8) {
+            uint32_t tmp[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int64_t c = c0 + (int64_t)u * kSkThreads;
-            if (c < nchunks) *(v4i_s *)(sh + (c / cpr) * xs + (c % cpr) * 16) = tmp[u];
+            for (int u = 0; u < 8; ++u) {
+                const int64_t w = w0 + (int64_t)u * kSkThreads;
+                tmp[u] = w < nw ? vw[w] : 0u;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int64_t w = w0 + (int64_t)u * kSkThreads;
+#pragma unroll
+                for (int e = 0; e < EPW; ++e) {
+                    const uint32_t idx = (uint32_t)(w * EPW + e);
+                    const uint32_t hi = __umulhi(magic, idx);
+                    const uint32_t p = (hi + ((idx - hi) >> 1)) >> (dl - 1), j = idx - p * vks;
+                    if (w < nw && j < (uint32_t)nvec && p < (uint32_t)g.K)
+                        *(elem_t *)(sh + j * xs + (int64_t)p * esz) =
+                            (elem_t)(tmp[u] >> (8 * esz * e));
+                }
+            }
+        }
+        // Zero each vector's bytes from K up to the 16-byte padded length.
+        const int64_t pad = kb - (int64_t)g.K * esz;
+        if (tid < nvec * 16 && (tid & 15) < pad)
+            sh[(tid >> 4) * xs + (int64_t)g.K * esz + (tid & 15)] = 0;
+    } else {
+        using elem_t = typename std::conditional<esz == 1, uint8_t,
+                         typename std::conditional<esz == 2, uint16_t, uint32_t>::type>::type;
+        const elem_t *ve = (const elem_t *)vec;
+        const int64_t epr = kb / esz, nel = nvec * epr;
+        for (int64_t c0 = tid; c0 < nel; c0 += kSkThreads * 8) {
+            elem_t tmp[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int64_t c = c0 + (int64_t)u * kSkThreads;
+                const int64_t j = c / epr, p = c % epr;
+                tmp[u] = (c < nel && p < g.K) ? ve[j * g.vld + p * g.vks] : (elem_t)0;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int64_t c = c0 + (int64_t)u * kSkThreads;
+                if (c < nel) *(elem_t *)(sh + (c / epr) * xs + (c % epr) * esz) = tmp[u];
+            }
         }
     }
     val_t *comb = (val_t *)(sh + nvec * xs);
     __syncthreads();
 
-    acc_t acc[2][kSkBlocks];
+    acc_t acc[2][BLK];
     // Multiplies batch t; after an item's last batch, forms each matrix row's
     // result from the two MFMAs, sums the four K ranges (wave order) through
     // LDS and applies the epilogue.
-    auto run = [&](int t, const v4i_s (&m)[kSkPF][kSkBlocks]) {
+    auto run = [&](int t, const v4i_s (&m)[kSkPF][BLK]) {
         const int q = t % nbw;
         if (q == 0) {
 #pragma unroll
-            for (int b = 0; b < kSkBlocks; ++b) acc[0][b] = acc[1][b] = acc_t{};
+            for (int b = 0; b < BLK; ++b) acc[0][b] = acc[1][b] = acc_t{};
         }
         const int s0 = ks0 + q * kSkPF;
 #pragma unroll
@@ -194,27 +266,25 @@ __global__ __launch_bounds__(kSkThreads) void skinny_mfma(const GemvArgs g, cons
                     v4i_s xv = *(const v4i_s *)(sh + xaddr + (int64_t)s * kSkStep + 16 * h);
                     if (!lvec || (int64_t)s * kSkStep + 16 * (2 * lg + h) >= kb) xv = v4i_s{0, 0, 0, 0};
 #pragma unroll
-                    for (int b = 0; b < kSkBlocks; ++b) acc[h][b] = Mm::step(m[p][b], xv, acc[h][b]);
+                    for (int b = 0; b < BLK; ++b) acc[h][b] = Mm::step(m[p][b], xv, acc[h][b]);
                 }
             }
         }
         if (q != nbw - 1) return;
         const int r0 = ((int)blockIdx.x + (t / nbw) * (int)gridDim.x) * kSkRows;
 #pragma unroll
-        for (int b = 0; b < kSkBlocks; ++b)
+        for (int b = 0; b < BLK; ++b)
 #pragma unroll
             for (int e = 0; e < 2; ++e)
-                comb[((wave * kSkBlocks + b) * 2 + e) * 64 + lane] =
+                comb[((wave * BLK + b) * 2 + e) * 64 + lane] =
                     (val_t)acc[0][b][2 * e] + (val_t)acc[1][b][2 * e + 1];
         __syncthreads();
-        constexpr int kPer = kSkBlocks * 2 / kSkWaves;  // 64-entry rows each wave sums
 #pragma unroll
-        for (int u = 0; u < kPer; ++u) {
-            const int x = (wave * kPer + u) * 64 + lane;  // over kSkBlocks*2*64
+        for (int x = tid; x < BLK * 2 * 64; x += kSkThreads) {
             const int b = x / 128, e = (x / 64) % 2, ln = x % 64;
             val_t sum = comb[x];
 #pragma unroll
-            for (int w = 1; w < kSkWaves; ++w) sum += comb[w * kSkBlocks * 2 * 64 + x];
+            for (int w = 1; w < kSkWaves; ++w) sum += comb[w * BLK * 2 * 64 + x];
             const int row = r0 + 8 * b + 2 * (ln >> 4) + e, j = ln & 15;
             if (j < nvec && row < g.R) Store<E>::apply(ep, 0, j, row, sum);
         }
@@ -239,14 +309,22 @@ int64_t skinny_lds_bytes(InType in, int64_t K, int nvec) {
 template <InType T, EpiKind E>
 static hipError_t skinny_go(const GemvArgs &g, const EpiParams &ep, hipStream_t stream) {
     const int64_t shm = skinny_lds_bytes(T, g.K, g.nvec);
-    const int64_t items = (g.R + kSkRows - 1) / kSkRows;
+    const int cus = g.cus > 0 ? g.cus : 256;
+    // 32-row items when there are enough of them for every CU, else 8-row
+    // items (4x as many workgroups streaming the same bytes).
+    const bool wide = (g.R + 31) / 32 >= cus;
+    const int64_t items = wide ? (g.R + 31) / 32 : (g.R + 7) / 8;
     // As many resident workgroups per CU as its 160 KiB of LDS holds (<= 4).
     const int fit = (int)(160 * 1024 / shm);
     const int per_cu = fit < 4 ? (fit > 1 ? fit : 1) : 4;
-    int64_t blocks = (int64_t)(g.cus > 0 ? g.cus : 256) * per_cu;
+    int64_t blocks = (int64_t)cus * per_cu;
     if (blocks > items) blocks = items;
-    hipLaunchKernelGGL((skinny_mfma<T, E>), dim3((unsigned)blocks), dim3(kSkThreads), (size_t)shm,
-                       stream, g, ep);
+    if (wide)
+        hipLaunchKernelGGL((skinny_mfma<T, E, 4>), dim3((unsigned)blocks), dim3(kSkThreads),
+                           (size_t)shm, stream, g, ep);
+    else
+        hipLaunchKernelGGL((skinny_mfma<T, E, 1>), dim3((unsigned)blocks), dim3(kSkThreads),
+                           (size_t)shm, stream, g, ep);
     return hipGetLastError();
 }
 

@@ -146,3 +146,65 @@ def test_batched_skinny_equals_loop(dev):
                             gk.MatRef(b[z * n * k:], k, n, 1, k), 0.0,
                             gk.MatMut.from_row_major(one, m, n))
         assert torch.equal(one, c[z * m * n:(z + 1) * m * n])
+
+
+@pytest.mark.parametrize("dtype", ["i8", "f32", "bf16"])
+@pytest.mark.parametrize("m", [2, 8, 16])
+def test_strided_vectors_small_batch(dev, dtype, m):
+    """gemmkit's fixed-weight inference shape (benches/gemm_bench.rs:380-470):
+    A (m x 2048) column-major -- vectors staged element by element, no pack --
+    against a 2048 x 2048 weight, plain and prepacked, C column-major."""
+    import torch
+    k = n = 2048
+    tdt = {"i8": torch.int8, "f32": torch.float32, "bf16": torch.bfloat16}[dtype]
+    g = torch.Generator().manual_seed(m)
+    if dtype == "i8":
+        a = torch.randint(-128, 128, (m * k,), dtype=torch.int8, generator=g)
+        b = torch.randint(-128, 128, (k * n,), dtype=torch.int8, generator=g)
+    else:
+        a = torch.randn(m * k, generator=g).to(tdt)
+        b = torch.randn(k * n, generator=g).to(tdt)
+    ad, bd = a.to(dev), b.to(dev)
+    A = gk.MatRef.from_col_major(ad, m, k)
+    if dtype == "i8":
+        B = gk.MatRef.from_col_major(bd, k, n)
+        c1 = torch.zeros(m * n, dtype=torch.int32, device=dev)
+        c2 = torch.zeros_like(c1)
+        gk.gemm_i8(1, A, B, 0, gk.MatMut.from_col_major(c1, m, n))
+        gk.gemm_i8_packed_b(1, A, gk.prepack_rhs_i8(B), 0, gk.MatMut.from_col_major(c2, m, n))
+        want = np.zeros(m * n, np.int32)
+        oracle.gemm_i8(m, k, n, 1, a.numpy(), 1, m, b.numpy(), 1, k, 0, want, 1, m)
+        assert np.array_equal(c1.cpu().numpy(), want)
+        assert torch.equal(c1, c2)
+        return
+    B = gk.MatRef.from_row_major(bd, k, n)
+    c1 = torch.zeros(m * n, dtype=tdt, device=dev)
+    c2 = torch.zeros_like(c1)
+    gk.gemm(1.0, A, B, 0.0, gk.MatMut.from_col_major(c1, m, n))
+    gk.gemm_packed_b(1.0, A, gk.prepack_rhs(B), 0.0, gk.MatMut.from_col_major(c2, m, n))
+    ints = torch.int32 if dtype == "f32" else torch.int16
+    assert torch.equal(c1.view(ints), c2.view(ints))
+    af = a.float().numpy() if dtype == "f32" else a.float().numpy()
+    ref = oracle.gemm_f64(m, k, n, 1.0, af, 1, m, b.float().numpy(), n, 1)
+    got = c1.float().cpu().numpy().reshape(n, m).T.astype(np.float64)
+    if dtype == "f32":
+        assert rel_frob(got, ref) <= 1e-5
+    else:
+        floor = 1e-3 * np.abs(ref).max()
+        assert (np.abs(got - ref) <= 2.0 ** -8 * np.maximum(np.abs(ref), floor)).all()
+
+
+@pytest.mark.parametrize("m,k,n", [(4, 300, 500), (16, 2048, 96), (3, 7, 40)])
+def test_negative_stride_vectors(dev, m, k, n):
+    """Unchecked tier: A walked backwards in both dimensions (rsa = -k, csa =
+    -1 from its last element) goes straight into the skinny kernel's
+    element-wise staging (tests/correctness/int8.rs:278-316 shape of test)."""
+    import torch
+    a = oracle.rand_i8_100(71 + m, m * k)
+    b = oracle.rand_i8_100(72 + n, k * n)
+    want = np.zeros(m * n, np.int32)
+    oracle.gemm_i8(m, k, n, 1, a, -k, -1, b, 1, k, 0, want, n, 1, a_off=m * k - 1)
+    c = torch.zeros(m * n, dtype=torch.int32, device=dev)
+    gk.gemm_i8_unchecked(m, k, n, 1, to_dev(a, dev), -k, -1, to_dev(b, dev), 1, k, 0, c, n, 1,
+                         a_off=m * k - 1)
+    assert np.array_equal(c.cpu().numpy(), want)
