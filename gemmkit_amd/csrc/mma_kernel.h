@@ -199,7 +199,13 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     using acc_t = typename M::acc_t;
     using val_t = typename M::scalar_t;
 
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
+    // One LDS object for everything (the stage ring, then the requantization
+    // channels): with a second __shared__ array the compiler can no longer
+    // tell the operand reads from the direct-to-LDS loads in flight and
+    // drains every load (vmcnt(0)) before each stage's fragment reads.
+    constexpr int QCH = (E == EpiKind::Q8) ? (BM > BN ? BM : BN) : 1;
+    constexpr int QBYTES = (E == EpiKind::Q8) ? QCH * 8 : 0;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM + QBYTES];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -334,20 +340,23 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     // in flight behind the prologue's stage loads (loads complete in order),
     // and reach LDS after the prologue wait; the main loop's barriers publish
     // them.
-    constexpr int QCH = (E == EpiKind::Q8) ? (BM > BN ? BM : BN) : 1;
-    __shared__ float q_scale[QCH];
-    __shared__ int32_t q_bias[QCH];
-    static_assert(E != EpiKind::Q8 || QCH <= NWAVES * 64, "one channel per thread");
+    constexpr int QPT = (QCH + NWAVES * 64 - 1) / (NWAVES * 64);  // channels per thread
+    float *const q_scale = (float *)(smem + SMEM);
+    int32_t *const q_bias = (int32_t *)(smem + SMEM + QCH * 4);
     int q_ch0 = 0, q_n = 0;
-    float q_s = 0.0f;
-    int32_t q_b = 0;
+    float q_s[QPT] = {};
+    int32_t q_b[QPT] = {};
     if constexpr (E == EpiKind::Q8) {
         q_n = ep.axis ? BN : BM;
         q_ch0 = ep.axis ? n0 : m0;
-        const int lim = ep.axis ? args.N : args.M, ch = q_ch0 + tid;
-        if (tid < q_n) {
-            q_s = ep.scales ? (ch < lim ? ep.scales[ch] : 1.0f) : ep.scale;
-            q_b = (ep.bias && ch < lim) ? ep.bias[ch] : 0;
+        const int lim = ep.axis ? args.N : args.M;
+#pragma unroll
+        for (int u = 0; u < QPT; ++u) {
+            const int c = tid + u * NWAVES * 64, ch = q_ch0 + c;
+            if (c < q_n) {
+                q_s[u] = ep.scales ? (ch < lim ? ep.scales[ch] : 1.0f) : ep.scale;
+                q_b[u] = (ep.bias && ch < lim) ? ep.bias[ch] : 0;
+            }
         }
     }
 
@@ -355,9 +364,13 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     for (int s0 = 0; s0 < NS - 1; ++s0) issue_stage(s0, s0, 0, NIW);
     wait_vmcnt<(NS - 2) * NIW>();
     if constexpr (E == EpiKind::Q8) {
-        if (tid < q_n) {
-            q_scale[tid] = q_s;
-            q_bias[tid] = q_b;
+#pragma unroll
+        for (int u = 0; u < QPT; ++u) {
+            const int c = tid + u * NWAVES * 64;
+            if (c < q_n) {
+                q_scale[c] = q_s[u];
+                q_bias[c] = q_b[u];
+            }
         }
     }
     stage_barrier();
