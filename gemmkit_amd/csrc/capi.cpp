@@ -335,31 +335,37 @@ bool skinny_enabled() {
 // Tile choice: the tile with the smallest makespan.  Tiles spread evenly over
 // the CUs, so the busiest CU runs per_cu = ceil(tiles / CUs) of them, up to
 // `occ` at a time.  A tile costs its main loop, BM*BN*kf / eff[n-1] (kf: K
-// bytes per row relative to 4096; n tiles sharing a CU deliver eff[n-1] of
-// its matrix-core peak), plus its epilogue, BM*BN*c_epi, of which a fraction
-// `hide` overlaps the next tile's main loop when the CU has more than one
-// (a second workgroup, or a second wave per SIMD, keeps the matrix cores busy
-// meanwhile); the last epilogue is never hidden.  Every tile also waits once
-// for its first stages to arrive (kTileLatency, ~2 us).  Calibrated on
-// measured int8 runs (4096^3; 2048 x 11008 x 4096 with i32 and requantized
-// output) and checked against bf16 batched 64 x 512 x 512 x 128 and small
-// f32/int8 squares.
-Tile pick_tile(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind kind) {
+// bytes per row relative to 4096, times the f32 matrix cores' lower rate for
+// f32 inputs; n tiles sharing a CU deliver eff[n-1] of its matrix-core peak),
+// plus its epilogue, BM*BN * c_epi(output kind) * epi (the tile's epilogue
+// speed: eight waves per CU finish it sooner), plus a fixed per-tile latency
+// (first stages in flight).  A fraction `hide` of the epilogue and latency
+// overlaps the next tile's main loop when a CU runs more than one; the last
+// is never hidden.  The constants are the fit of gemmkit_amd/calibrate_tiles.py
+// to graph-timed runs of 13 shapes x 6 tiles (int8 i32 and requantized, bf16
+// with f32 and bf16 output, batched attention scores, f32; 1024^2 to 4096^3
+// and 2048 x 11008 x 4096): least squares on log time, then refined so the
+// chosen tile is within noise of the best measured one on each shape.
+Tile pick_tile(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind kind, InType in) {
     bool forced;
     Tile t = env_tile(&forced);
     if (forced) return t;
-    struct Cand { Tile t; int bm, bn, occ; double eff[2], hide; };
+    struct Cand { Tile t; int bm, bn, occ; double eff[2], hide, epi; };
     static const Cand cands[] = {
-        {Tile::T256x256, 256, 256, 1, {0.83, 0.83}, 0.0},
-        {Tile::T256x256w8, 256, 256, 1, {0.81, 0.81}, 0.6},
-        {Tile::T256x128o2, 256, 128, 2, {0.45, 0.60}, 0.5},
-        {Tile::T256x128, 256, 128, 1, {0.55, 0.55}, 0.0},
-        {Tile::T128x128, 128, 128, 2, {0.35, 0.50}, 0.5},
-        {Tile::T64x64, 64, 64, 2, {0.20, 0.30}, 0.5},
+        {Tile::T256x256, 256, 256, 1, {0.7596, 0.7596}, 0.4037, 1.0},
+        {Tile::T256x256w8, 256, 256, 1, {0.8986, 0.8986}, 0.3792, 1.0006},
+        {Tile::T256x128o2, 256, 128, 2, {0.6262, 0.5576}, 0.6324, 0.4541},
+        {Tile::T256x128, 256, 128, 1, {0.6151, 0.6151}, 0.4778, 0.7034},
+        {Tile::T128x128, 128, 128, 2, {0.6608, 0.4713}, 0.8791, 0.2},
+        {Tile::T64x64, 64, 64, 2, {0.591, 0.3571}, 0.9196, 3.0},
     };
-    const double c_epi = kind == EpiKind::Q8 ? 0.97 : (kind == EpiKind::BF16 ? 0.2 : 0.28);
-    constexpr double kTileLatency = 4000.0;  // in the units of area / eff
-    const double kf = (double)std::max<int64_t>(kbytes, 64) / 4096.0;
+    const double c_epi = kind == EpiKind::Q8 ? 0.7537
+                         : kind == EpiKind::I32 ? 0.3834
+                         : kind == EpiKind::F32 ? 0.1512 : 0.0;
+    constexpr double kTileLatency = 22391.6;  // in the units of area / eff
+    constexpr double kF32Rate = 4.481;        // f32 main-loop cost per K byte vs i8/bf16
+    const double kf = (double)std::max<int64_t>(kbytes, 64) / 4096.0 *
+                      (in == InType::F32 ? kF32Rate : 1.0);
     double best = 1e300;
     Tile bt = Tile::T64x64;
     const int64_t cus = g_num_cus > 0 ? g_num_cus : 256;
@@ -370,7 +376,7 @@ Tile pick_tile(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind kind
         const double area = (double)c.bm * c.bn;
         const double exposed = per_cu - c.hide * (per_cu - 1);
         const double cost = per_cu * area * kf / c.eff[together - 1] +
-                            (area * c_epi + kTileLatency) * exposed;
+                            (area * c_epi * c.epi + kTileLatency) * exposed;
         if (cost < best * 0.999) { best = cost; bt = c.t; }
     }
     return bt;
@@ -548,7 +554,7 @@ int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t
         if (e != hipSuccess) return hip_fail(e, "split reduce launch");
         return finish("mfma gemm (split K)");
     }
-    e = launch_mma(in, pick_tile(M, N, batch, k * (int64_t)esz, ep.kind), args, ep, tl_stream);
+    e = launch_mma(in, pick_tile(M, N, batch, k * (int64_t)esz, ep.kind, in), args, ep, tl_stream);
     if (e != hipSuccess) return hip_fail(e, "mfma launch");
     return finish("mfma gemm");
 }
