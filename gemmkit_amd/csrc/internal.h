@@ -62,8 +62,8 @@ struct MmaArgs {
     int32_t M, N, K;       // K in elements
     int32_t batch;
     // Split K (1 = off): K range r = [r*kchunk, min(K, (r+1)*kchunk)) of batch
-    // element b writes its partial sums to output slab b*splits + r; kchunk
-    // is a multiple of 64 bytes of K.
+    // element b (grid y = r, z = b) writes its partial sums to output slab
+    // b*splits + r; kchunk is a multiple of 64 bytes of K.
     int32_t splits, kchunk;
 };
 

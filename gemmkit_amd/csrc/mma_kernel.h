@@ -217,15 +217,16 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     int tmi, tni;
     tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tmi, tni);
     const int m0 = tmi * BM, n0 = tni * BN;
-    // Output slab z.  SPLIT: z = batch element * splits + K range, and each
-    // range's partial sums go to a slab of their own (the epilogue's batch
-    // stride), to be reduced in range order afterwards.  The unsplit kernels
-    // are separate instantiations, so their code is untouched by this.
-    const int64_t z = blockIdx.z;
-    int64_t zb = z, k0 = 0, kel = args.K;
+    // Batch element zb = blockIdx.z, output slab z.  SPLIT: K range
+    // blockIdx.y, and each range's partial sums go to a slab of their own,
+    // z = zb * splits + range (the epilogue's batch stride), to be reduced in
+    // range order afterwards.  The unsplit kernels are separate
+    // instantiations, so their code is untouched by this.
+    const int64_t zb = blockIdx.z;
+    int64_t z = zb, k0 = 0, kel = args.K;
     if constexpr (SPLIT) {
-        zb = z / args.splits;
-        k0 = (z % args.splits) * (int64_t)args.kchunk;
+        z = zb * args.splits + blockIdx.y;
+        k0 = (int64_t)blockIdx.y * args.kchunk;
         kel = args.K - k0 < args.kchunk ? args.K - k0 : args.kchunk;
     }
 
@@ -511,7 +512,7 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
 template <InType T, EpiKind E, int BM, int BN, int WM, int WN, int NS, bool SPLIT = false>
 static hipError_t launch_one(const MmaArgs &args, const EpiParams &ep, hipStream_t stream) {
     int tiles = ((args.M + BM - 1) / BM) * ((args.N + BN - 1) / BN);
-    dim3 grid(tiles, 1, args.batch * (SPLIT ? args.splits : 1));
+    dim3 grid(tiles, SPLIT ? args.splits : 1, args.batch);
     hipLaunchKernelGGL((mma_kernel<T, E, BM, BN, WM, WN, 64, NS, SPLIT>), grid,
                        dim3(WM * WN * 64), 0, stream, args, ep);
     return hipGetLastError();
