@@ -131,7 +131,9 @@ class Workspace:
     """Workspace (src/workspace.rs:53): a device scratch arena owned by the caller."""
 
     def __init__(self) -> None:
-        self._h = _lib.lib().gk_workspace_new()
+        L = _lib.lib()
+        self._free = L.gk_workspace_free  # held so __del__ works during interpreter exit
+        self._h = L.gk_workspace_new()
 
     @property
     def handle(self):
@@ -143,7 +145,7 @@ class Workspace:
     def __del__(self) -> None:
         h, self._h = getattr(self, "_h", None), None
         if h:
-            _lib.lib().gk_workspace_free(h)
+            self._free(h)
 
 
 def _ws(ws: Optional[Workspace]):
@@ -382,6 +384,7 @@ class PackedRhs:
     (i8 from :func:`prepack_rhs_i8`, f32/bf16 from :func:`prepack_rhs`)."""
 
     def __init__(self, handle):
+        self._free = _lib.lib().gk_packed_rhs_free  # held so __del__ works during interpreter exit
         self._h = handle
 
     @property
@@ -397,7 +400,7 @@ class PackedRhs:
     def __del__(self) -> None:
         h, self._h = getattr(self, "_h", None), None
         if h:
-            _lib.lib().gk_packed_rhs_free(h)
+            self._free(h)
 
 
 def prepack_rhs_i8(b: MatRef) -> PackedRhs:
