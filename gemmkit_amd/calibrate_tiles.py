@@ -21,7 +21,8 @@ import json
 import os
 
 TILES = {"256x256": (256, 256, 1), "256x256w8": (256, 256, 1), "256x128o2": (256, 128, 2),
-         "256x128": (256, 128, 1), "128x128": (128, 128, 2), "64x64": (64, 64, 2)}
+         "256x128": (256, 128, 1), "128x128": (128, 128, 2), "64x64": (64, 64, 2),
+         "256x256k128": (256, 256, 1)}
 KINDS = ["i32", "q8", "f32", "bf16"]
 CUS = 256
 
@@ -131,13 +132,16 @@ def fit(path: str) -> None:
     occ2 = [t for t in tn if TILES[t][2] == 2]
     pts = [(d["meta"], t, d["us"][t]) for d in data.values() for t in tn]
 
+    nt = len(tn)
+
     def unpack(p):
-        e1 = dict(zip(tn, p[0:6]))
-        e2 = dict(zip(occ2, p[6:9]))
-        hd = dict(zip(tn, p[9:15]))
-        ce = dict(zip(KINDS, p[15:19]))
-        lat, rf, s = p[19], p[20], p[21]
-        es = dict(zip(tn, [1.0] + list(p[22:27])))
+        i = 0
+        e1 = dict(zip(tn, p[i:i + nt])); i += nt
+        e2 = dict(zip(occ2, p[i:i + len(occ2)])); i += len(occ2)
+        hd = dict(zip(tn, p[i:i + nt])); i += nt
+        ce = dict(zip(KINDS, p[i:i + 4])); i += 4
+        lat, rf, s = p[i], p[i + 1], p[i + 2]; i += 3
+        es = dict(zip(tn, [1.0] + list(p[i:i + nt - 1])))
         return e1, e2, hd, ce, lat, rf, s, es
 
     def model(p, meta, t):
@@ -154,39 +158,51 @@ def fit(path: str) -> None:
     def resid(p):
         return [np.log(model(p, m, t) / us) for m, t, us in pts]
 
+    def pick(p, meta):
+        # pick_tile's rule: candidates in order, a later one must be 0.1% cheaper
+        best, bt = float("inf"), None
+        for t in tn:
+            c = model(p, meta, t)
+            if c < best * 0.999:
+                best, bt = c, t
+        return bt
+
     def regret(p):
         tot = 0.0
         for d in data.values():
-            pred = min(tn, key=lambda t: model(p, d["meta"], t))
-            tot += d["us"][pred] / min(d["us"][t] for t in tn) - 1
+            tot += d["us"][pick(p, d["meta"])] / min(d["us"][t] for t in tn) - 1
         return tot
 
-    p0 = [0.83, 0.81, 0.45, 0.55, 0.35, 0.2, 0.6, 0.5, 0.3, 0.0, 0.6, 0.5, 0.0, 0.5, 0.5,
-          0.28, 0.5, 0.28, 0.2, 4000, 8, 0.00076] + [1.0] * 5
-    lo = [0.05] * 9 + [0.0] * 6 + [0.0] * 4 + [0, 1, 1e-5] + [0.2] * 5
-    hi = [1.0] * 9 + [1.0] * 6 + [3.0] * 4 + [50000, 30, 1e-2] + [3.0] * 5
-    best = least_squares(resid, p0, bounds=(lo, hi)).x
-    rng = np.random.default_rng(0)
+    p0 = [0.7] * nt + [0.5] * len(occ2) + [0.5] * nt + [0.3, 0.5, 0.3, 0.2, 4000, 4, 0.0005] + \
+        [1.0] * (nt - 1)
+    lo = [0.05] * (nt + len(occ2)) + [0.0] * nt + [0.0] * 4 + [0, 1, 1e-5] + [0.2] * (nt - 1)
+    hi = [1.0] * (nt + len(occ2)) + [1.0] * nt + [3.0] * 4 + [50000, 30, 1e-2] + [3.0] * (nt - 1)
+    start = least_squares(resid, p0, bounds=(lo, hi)).x
     obj = lambda p: regret(p) + 0.2 * np.sqrt(np.mean(np.square(resid(p))))  # noqa: E731
-    bo = obj(best)
-    for _ in range(6000):
-        q = best.copy()
-        k = rng.integers(len(q))
-        q[k] = np.clip(q[k] * np.exp(rng.normal(0, 0.15)), lo[k], hi[k])
-        o = obj(q)
-        if o < bo:
-            best, bo = q, o
+    best, bo = start, obj(start)
+    for seed in range(6):  # random-walk refinements from the least-squares fit
+        rng = np.random.default_rng(seed)
+        cur, co = start.copy(), obj(start)
+        for _ in range(5000):
+            q = cur.copy()
+            k = rng.integers(len(q))
+            q[k] = np.clip(q[k] * np.exp(rng.normal(0, 0.2)), lo[k], hi[k])
+            o = obj(q)
+            if o < co:
+                cur, co = q, o
+        if co < bo:
+            best, bo = cur, co
     e1, e2, hd, ce, lat, rf, s, es = unpack(best)
-    print("eff (one tile / two sharing a CU):", {t: (round(e1[t], 4), round(e2.get(t, e1[t]), 4))
+    print("eff (one tile / two sharing a CU):", {t: (round(e1[t], 6), round(e2.get(t, e1[t]), 6))
                                                 for t in tn})
-    print("hide:", {t: round(hd[t], 4) for t in tn})
-    print("epilogue speed:", {t: round(es[t], 4) for t in tn})
-    print("c_epi:", {k: round(v, 4) for k, v in ce.items()}, "latency", round(lat, 1),
-          "f32 rate", round(rf, 3))
+    print("hide:", {t: round(hd[t], 6) for t in tn})
+    print("epilogue speed:", {t: round(es[t], 6) for t in tn})
+    print("c_epi:", {k: round(v, 6) for k, v in ce.items()}, "latency", round(lat, 3),
+          "f32 rate", round(rf, 6))
     print("regret", round(regret(best), 4), "rms log error",
           round(float(np.sqrt(np.mean(np.square(resid(best))))), 4))
     for name, d in data.items():
-        pred = min(tn, key=lambda t: model(best, d["meta"], t))
+        pred = pick(best, d["meta"])
         bm = min(tn, key=lambda t: d["us"][t])
         print(f"{name:22s} pick {pred:10s} {d['us'][pred]:8.2f} us   best {bm:10s} "
               f"{d['us'][bm]:8.2f} us")

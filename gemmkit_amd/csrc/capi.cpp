@@ -321,6 +321,7 @@ Tile env_tile(bool *forced) {
     if (!strcmp(s, "256x128")) return Tile::T256x128;
     if (!strcmp(s, "128x128")) return Tile::T128x128;
     if (!strcmp(s, "64x64")) return Tile::T64x64;
+    if (!strcmp(s, "256x256k128")) return Tile::T256x256k128;
     *forced = false;
     return Tile::T256x256;
 }
@@ -352,18 +353,19 @@ Tile pick_tile(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind kind
     if (forced) return t;
     struct Cand { Tile t; int bm, bn, occ; double eff[2], hide, epi; };
     static const Cand cands[] = {
-        {Tile::T256x256, 256, 256, 1, {0.7596, 0.7596}, 0.4037, 1.0},
-        {Tile::T256x256w8, 256, 256, 1, {0.8986, 0.8986}, 0.3792, 1.0006},
-        {Tile::T256x128o2, 256, 128, 2, {0.6262, 0.5576}, 0.6324, 0.4541},
-        {Tile::T256x128, 256, 128, 1, {0.6151, 0.6151}, 0.4778, 0.7034},
-        {Tile::T128x128, 128, 128, 2, {0.6608, 0.4713}, 0.8791, 0.2},
-        {Tile::T64x64, 64, 64, 2, {0.591, 0.3571}, 0.9196, 3.0},
+        {Tile::T256x256, 256, 256, 1, {0.897294, 0.897294}, 0.409392, 1.0},
+        {Tile::T256x256w8, 256, 256, 1, {0.923286, 0.923286}, 0.343645, 0.73611},
+        {Tile::T256x128o2, 256, 128, 2, {0.743398, 0.641614}, 0.67192, 0.61994},
+        {Tile::T256x128, 256, 128, 1, {0.698244, 0.698244}, 0.432022, 0.580563},
+        {Tile::T128x128, 128, 128, 2, {0.769761, 0.526235}, 0.873501, 0.228047},
+        {Tile::T64x64, 64, 64, 2, {0.748085, 0.400346}, 0.917687, 3.0},
+        {Tile::T256x256k128, 256, 256, 1, {0.926765, 0.926765}, 0.140032, 0.740587},
     };
-    const double c_epi = kind == EpiKind::Q8 ? 0.7537
-                         : kind == EpiKind::I32 ? 0.3834
-                         : kind == EpiKind::F32 ? 0.1512 : 0.0;
-    constexpr double kTileLatency = 22391.6;  // in the units of area / eff
-    constexpr double kF32Rate = 4.481;        // f32 main-loop cost per K byte vs i8/bf16
+    const double c_epi = kind == EpiKind::Q8 ? 0.811672
+                         : kind == EpiKind::I32 ? 0.395869
+                         : kind == EpiKind::F32 ? 0.19742 : 0.174441;
+    constexpr double kTileLatency = 20500.992;  // in the units of area / eff
+    constexpr double kF32Rate = 4.680181;    // f32 main-loop cost per K byte vs i8/bf16
     const double kf = (double)std::max<int64_t>(kbytes, 64) / 4096.0 *
                       (in == InType::F32 ? kF32Rate : 1.0);
     double best = 1e300;

@@ -377,39 +377,94 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     stage_barrier();
     read_frags(smem, 0, 0);
 
-    static_assert(SUB == 2, "schedule assumes two sub-steps");
-    for (int kt = 0; kt < KT; ++kt) {
-        const uint8_t *s = smem + (kt % NS) * STAGE;
-        const int nslot = (kt + NS - 1) % NS;
-        read_frags(s, 1, 1);
-        mfmas(0);
-        issue_stage(kt + NS - 1, nslot, 0, H0);
-#pragma unroll
-        for (int i = 0; i < TM * TN; ++i) {
-            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-            if (i < TM + TN) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-            if (i >= TM * TN - H0) __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
+    if constexpr (SUB == 2) {
+        for (int kt = 0; kt < KT; ++kt) {
+            const uint8_t *s = smem + (kt % NS) * STAGE;
+            const int nslot = (kt + NS - 1) % NS;
+            read_frags(s, 1, 1);
+            mfmas(0);
+            issue_stage(kt + NS - 1, nslot, 0, H0);
+    #pragma unroll
+            for (int i = 0; i < TM * TN; ++i) {
+                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+                if (i < TM + TN) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+                if (i >= TM * TN - H0) __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
+            }
+    #pragma unroll
+            for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[0][i]));
+    #pragma unroll
+            for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bf[0][j]));
+            // Stage kt+1's loads were issued at iteration kt+2-NS; issued after
+            // them: NS-3 whole iterations plus this phase A.
+            wait_vmcnt<(NS - 3) * NIW + H0>();
+            stage_barrier();
+    #pragma unroll
+            for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[1][i]));
+    #pragma unroll
+            for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bf[1][j]));
+            read_frags(smem + ((kt + 1) % NS) * STAGE, 0, 0);
+            mfmas(1);
+            issue_stage(kt + NS - 1, nslot, H0, H1);
+    #pragma unroll
+            for (int i = 0; i < TM * TN; ++i) {
+                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+                if (i < TM + TN) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+                if (i >= TM * TN - H1) __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
+            }
         }
+    } else {
+        // 128-byte stages in a two-stage ring: each row of a stage is one
+        // whole 128-byte line of K (half the cache-line requests of two
+        // 64-byte stages) and one barrier covers four sub-steps.  The next
+        // stage's loads go out at the start of the current one, into the slot
+        // every wave finished reading before the previous barrier; its first
+        // fragments are read under the last sub-step's MFMAs, as above.
+        static_assert(SUB == 4 && NS == 2, "four sub-steps run with a two-stage ring");
+        for (int kt = 0; kt < KT; ++kt) {
+            const uint8_t *s = smem + (kt & 1) * STAGE;
+            const int nslot = (kt + 1) & 1;
+            read_frags(s, 1, 1);
+            mfmas(0);
+            issue_stage(kt + 1, nslot, 0, H0);
 #pragma unroll
-        for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[0][i]));
+            for (int i = 0; i < TM * TN; ++i) {
+                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+                if (i < TM + TN) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+                if (i >= TM * TN - H0) __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
+            }
+            read_frags(s, 2, 0);
+            mfmas(1);
+            issue_stage(kt + 1, nslot, H0, H1);
 #pragma unroll
-        for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bf[0][j]));
-        // Stage kt+1's loads were issued at iteration kt+2-NS; issued after
-        // them: NS-3 whole iterations plus this phase A.
-        wait_vmcnt<(NS - 3) * NIW + H0>();
-        stage_barrier();
+            for (int i = 0; i < TM * TN; ++i) {
+                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+                if (i < TM + TN) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+                if (i >= TM * TN - H1) __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
+            }
+            read_frags(s, 3, 1);
+            mfmas(0);
 #pragma unroll
-        for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[1][i]));
+            for (int i = 0; i < TM * TN; ++i) {
+                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+                if (i < TM + TN) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+            }
 #pragma unroll
-        for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bf[1][j]));
-        read_frags(smem + ((kt + 1) % NS) * STAGE, 0, 0);
-        mfmas(1);
-        issue_stage(kt + NS - 1, nslot, H0, H1);
+            for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[0][i]));
 #pragma unroll
-        for (int i = 0; i < TM * TN; ++i) {
-            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-            if (i < TM + TN) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-            if (i >= TM * TN - H1) __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
+            for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bf[0][j]));
+            wait_vmcnt<0>();
+            stage_barrier();
+#pragma unroll
+            for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[1][i]));
+#pragma unroll
+            for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bf[1][j]));
+            read_frags(smem + nslot * STAGE, 0, 0);
+            mfmas(1);
+#pragma unroll
+            for (int i = 0; i < TM * TN; ++i) {
+                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+                if (i < TM + TN) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+            }
         }
     }
 
@@ -509,11 +564,12 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     }
 }
 
-template <InType T, EpiKind E, int BM, int BN, int WM, int WN, int NS, bool SPLIT = false>
+template <InType T, EpiKind E, int BM, int BN, int WM, int WN, int NS, bool SPLIT = false,
+          int BK = 64>
 static hipError_t launch_one(const MmaArgs &args, const EpiParams &ep, hipStream_t stream) {
     int tiles = ((args.M + BM - 1) / BM) * ((args.N + BN - 1) / BN);
     dim3 grid(tiles, SPLIT ? args.splits : 1, args.batch);
-    hipLaunchKernelGGL((mma_kernel<T, E, BM, BN, WM, WN, 64, NS, SPLIT>), grid,
+    hipLaunchKernelGGL((mma_kernel<T, E, BM, BN, WM, WN, BK, NS, SPLIT>), grid,
                        dim3(WM * WN * 64), 0, stream, args, ep);
     return hipGetLastError();
 }
@@ -536,6 +592,7 @@ static hipError_t launch_tile(Tile tile, const MmaArgs &args, const EpiParams &e
     case Tile::T256x128o2: return launch_one<T, E, 256, 128, 2, 2, 3>(args, ep, stream);
     case Tile::T128x128: return launch_one<T, E, 128, 128, 2, 2, 4>(args, ep, stream);
     case Tile::T64x64: return launch_one<T, E, 64, 64, 2, 2, 4>(args, ep, stream);
+    case Tile::T256x256k128: return launch_one<T, E, 256, 256, 2, 2, 2, false, 128>(args, ep, stream);
     }
     return hipErrorInvalidValue;
 }
