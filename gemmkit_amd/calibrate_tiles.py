@@ -22,7 +22,7 @@ import os
 
 TILES = {"256x256": (256, 256, 1), "256x256w8": (256, 256, 1), "256x128o2": (256, 128, 2),
          "256x128": (256, 128, 1), "128x128": (128, 128, 2), "64x64": (64, 64, 2),
-         "256x256k128": (256, 256, 1)}
+         "256x256k128": (256, 256, 1), "256x256w8k128": (256, 256, 1)}
 KINDS = ["i32", "q8", "f32", "bf16"]
 CUS = 256
 

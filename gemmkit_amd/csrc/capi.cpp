@@ -322,6 +322,7 @@ Tile env_tile(bool *forced) {
     if (!strcmp(s, "128x128")) return Tile::T128x128;
     if (!strcmp(s, "64x64")) return Tile::T64x64;
     if (!strcmp(s, "256x256k128")) return Tile::T256x256k128;
+    if (!strcmp(s, "256x256w8k128")) return Tile::T256x256w8k128;
     *forced = false;
     return Tile::T256x256;
 }
@@ -343,7 +344,7 @@ bool skinny_enabled() {
 // (first stages in flight).  A fraction `hide` of the epilogue and latency
 // overlaps the next tile's main loop when a CU runs more than one; the last
 // is never hidden.  The constants are the fit of gemmkit_amd/calibrate_tiles.py
-// to graph-timed runs of 13 shapes x 6 tiles (int8 i32 and requantized, bf16
+// to graph-timed runs of 13 shapes x 8 tiles (int8 i32 and requantized, bf16
 // with f32 and bf16 output, batched attention scores, f32; 1024^2 to 4096^3
 // and 2048 x 11008 x 4096): least squares on log time, then refined so the
 // chosen tile is within noise of the best measured one on each shape.
@@ -353,19 +354,20 @@ Tile pick_tile(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind kind
     if (forced) return t;
     struct Cand { Tile t; int bm, bn, occ; double eff[2], hide, epi; };
     static const Cand cands[] = {
-        {Tile::T256x256, 256, 256, 1, {0.897294, 0.897294}, 0.409392, 1.0},
-        {Tile::T256x256w8, 256, 256, 1, {0.923286, 0.923286}, 0.343645, 0.73611},
-        {Tile::T256x128o2, 256, 128, 2, {0.743398, 0.641614}, 0.67192, 0.61994},
-        {Tile::T256x128, 256, 128, 1, {0.698244, 0.698244}, 0.432022, 0.580563},
-        {Tile::T128x128, 128, 128, 2, {0.769761, 0.526235}, 0.873501, 0.228047},
-        {Tile::T64x64, 64, 64, 2, {0.748085, 0.400346}, 0.917687, 3.0},
-        {Tile::T256x256k128, 256, 256, 1, {0.926765, 0.926765}, 0.140032, 0.740587},
+        {Tile::T256x256, 256, 256, 1, {0.881972, 0.881972}, 0.408704, 1.0},
+        {Tile::T256x256w8, 256, 256, 1, {1.0, 1.0}, 0.435266, 0.870287},
+        {Tile::T256x128o2, 256, 128, 2, {0.771698, 0.648456}, 0.751995, 0.804527},
+        {Tile::T256x128, 256, 128, 1, {0.710394, 0.710394}, 0.502005, 0.636165},
+        {Tile::T128x128, 128, 128, 2, {0.818596, 0.571382}, 0.885997, 0.2},
+        {Tile::T64x64, 64, 64, 2, {0.817629, 0.413534}, 0.926261, 3.0},
+        {Tile::T256x256k128, 256, 256, 1, {0.840252, 0.840252}, 0.361402, 0.901789},
+        {Tile::T256x256w8k128, 256, 256, 1, {1.0, 1.0}, 0.342395, 0.847936},
     };
-    const double c_epi = kind == EpiKind::Q8 ? 0.811672
-                         : kind == EpiKind::I32 ? 0.395869
-                         : kind == EpiKind::F32 ? 0.19742 : 0.174441;
-    constexpr double kTileLatency = 20500.992;  // in the units of area / eff
-    constexpr double kF32Rate = 4.680181;    // f32 main-loop cost per K byte vs i8/bf16
+    const double c_epi = kind == EpiKind::Q8 ? 0.354519
+                         : kind == EpiKind::I32 ? 0.344598
+                         : kind == EpiKind::F32 ? 0.1222 : 0.063011;
+    constexpr double kTileLatency = 21811.149;  // in the units of area / eff
+    constexpr double kF32Rate = 4.823842;    // f32 main-loop cost per K byte vs i8/bf16
     const double kf = (double)std::max<int64_t>(kbytes, 64) / 4096.0 *
                       (in == InType::F32 ? kF32Rate : 1.0);
     double best = 1e300;

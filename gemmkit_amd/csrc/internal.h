@@ -76,6 +76,7 @@ enum class Tile : int {
     T256x256w8 = 4,
     T256x128o2 = 5,  // 3-stage ring: two workgroups per CU
     T256x256k128 = 6,  // 128-byte stages, 2-stage ring
+    T256x256w8k128 = 7,  // 8 waves, 128-byte stages, 2-stage ring
 };
 
 hipError_t launch_mma_i8(Tile tile, const MmaArgs &args, const EpiParams &ep, hipStream_t stream);

@@ -593,6 +593,7 @@ static hipError_t launch_tile(Tile tile, const MmaArgs &args, const EpiParams &e
     case Tile::T128x128: return launch_one<T, E, 128, 128, 2, 2, 4>(args, ep, stream);
     case Tile::T64x64: return launch_one<T, E, 64, 64, 2, 2, 4>(args, ep, stream);
     case Tile::T256x256k128: return launch_one<T, E, 256, 256, 2, 2, 2, false, 128>(args, ep, stream);
+    case Tile::T256x256w8k128: return launch_one<T, E, 256, 256, 2, 4, 2, false, 128>(args, ep, stream);
     }
     return hipErrorInvalidValue;
 }
