@@ -29,6 +29,8 @@
 //     current stage's second half of MFMAs run.
 // The 32x32 accumulator block lives in 16 registers per lane: register r of
 // lane l holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+#include <type_traits>
+
 #include "epilogue.h"
 
 namespace gk {
@@ -124,6 +126,55 @@ __device__ __forceinline__ void dma16(const uint8_t *base, uint32_t num, uint32_
         __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)num, kRsrcWord3);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16,
                                              voff, 0, 0, 0);
+}
+
+// The same with a wave-uniform byte offset `soff` added in the scalar operand:
+// no per-lane address arithmetic.  The range check may leave `soff` out, so
+// the caller guarantees that every lane with voff < num stays inside the
+// resource with soff added, and that lanes meant to read zeros have
+// voff >= num.
+__device__ __forceinline__ void dma16s(const uint8_t *base, uint32_t num, uint32_t voff,
+                                       uint32_t soff, uint8_t *lds) {
+    __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)num, kRsrcWord3);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16,
+                                             voff, (int)soff, 0, 0);
+}
+
+// A sub-step's memory operations in program order: NR fragment reads with NL
+// direct-to-LDS loads spread among them (a load after read r when
+// (r+1)*NL/NR > r*NL/NR).  The compiler cannot tell a load's LDS destination
+// from the reads' sources, so it keeps the two in program order; writing them
+// interleaved is what lets the schedule below interleave them.
+template <int NR, int NL>
+__device__ constexpr bool op_is_load(int o) {
+    int pos = 0;
+    for (int r = 0; r < NR; ++r) {
+        if (pos++ == o) return false;
+        if ((r + 1) * NL / NR != r * NL / NR && pos++ == o) return true;
+    }
+    return false;
+}
+
+// Schedule of one sub-step: NM MFMAs with the NR + NL operations above spread
+// over the first SPAN of them (the reads feed the next sub-step, so they go
+// out early).
+template <int NM, int NR, int NL, int SPAN>
+__device__ __forceinline__ void sched_ops() {
+    constexpr int NOPS = NR + NL;
+#pragma unroll
+    for (int i = 0; i < NM; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+#pragma unroll
+        for (int o = 0; o < NOPS; ++o) {
+            if (o * SPAN / NOPS == i) {
+                if (op_is_load<NR, NL>(o))
+                    __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
+                else
+                    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+            }
+        }
+    }
 }
 
 // A stage holds BK bytes of K for every A and B row of the tile: row r at
@@ -282,6 +333,30 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
             dma16(from_a[i] ? a_pan : b_pan, from_a[i] ? a_num : b_num, off, dst + i * 1024);
         }
     };
+    // Loads of a stage wholly inside K: the stage offset goes in the scalar
+    // operand.  Allowed when rows do not overlap (row stride >= the row's
+    // 16-byte-rounded length), so rows past the matrix edge start at or past
+    // their resource's end and read zeros whatever the offset, and the valid
+    // rows' bytes of a whole stage lie inside the resource.  When every wave's
+    // rows come from one operand (the tiles here but 256x128), the wave keeps
+    // one resource.
+    constexpr bool WAVE_OP = (BM % (NIW * RPI)) == 0;
+    const bool w_from_a = wave * NIW * RPI < BM;
+    const uint8_t *const w_pan = w_from_a ? a_pan : b_pan;
+    const uint32_t w_num = w_from_a ? a_num : b_num;
+    const bool soff_ok = lda_b >= kb16 && ldb_b >= kb16;
+    auto issue_whole = [&](int kt, int slot, int first, int count) {
+        const uint32_t kb = (uint32_t)kt * BK;
+        uint8_t *dst = smem + slot * STAGE + wave * NIW * 1024;
+#pragma unroll
+        for (int i = first; i < first + count; ++i) {
+            if constexpr (WAVE_OP)
+                dma16s(w_pan, w_num, voff[i], kb, dst + i * 1024);
+            else
+                dma16s(from_a[i] ? a_pan : b_pan, from_a[i] ? a_num : b_num, voff[i], kb,
+                       dst + i * 1024);
+        }
+    };
 
     acc_t acc[TM][TN];
 #pragma unroll
@@ -334,6 +409,11 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     // The empty asm statements pin F0 and F1 around the barrier so the compiler
     // keeps each phase's MFMAs on its side.
     constexpr int H0 = NIW / 2, H1 = NIW - H0;  // loads issued in phase A / C
+    // 128-byte stages: a stage's loads in three parts, after the barrier that
+    // frees its slot (P0) and under the next two sub-steps (P1, P2).  (Four
+    // parts, one per sub-step, measured slower: the last part then has too
+    // little time to land.)
+    constexpr int P0 = (NIW + 2) / 3, P1 = (NIW - P0 + 1) / 2, P2 = NIW - P0 - P1;
 
     // Requantization: the tile's channels (rows for a per-row map, columns
     // for a per-column one) get their scale and bias staged in LDS, so the
@@ -361,9 +441,17 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
         }
     }
 
+    if constexpr (SUB == 2) {
 #pragma unroll
-    for (int s0 = 0; s0 < NS - 1; ++s0) issue_stage(s0, s0, 0, NIW);
-    wait_vmcnt<(NS - 2) * NIW>();
+        for (int s0 = 0; s0 < NS - 1; ++s0) issue_stage(s0, s0, 0, NIW);
+        wait_vmcnt<(NS - 2) * NIW>();
+    } else {
+        // Stage 0 whole, and the first part of stage 1 (the main loop issues
+        // the rest of each stage, and the first part of the one after it).
+        issue_stage(0, 0, 0, NIW);
+        issue_stage(1, 1, 0, P0);
+        wait_vmcnt<P0>();
+    }
     if constexpr (E == EpiKind::Q8) {
 #pragma unroll
         for (int u = 0; u < QPT; ++u) {
@@ -415,39 +503,60 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     } else {
         // 128-byte stages in a two-stage ring: each row of a stage is one
         // whole 128-byte line of K (half the cache-line requests of two
-        // 64-byte stages) and one barrier covers four sub-steps.  The next
-        // stage's loads go out at the start of the current one, into the slot
-        // every wave finished reading before the previous barrier; its first
-        // fragments are read under the last sub-step's MFMAs, as above.
+        // 64-byte stages) and one barrier covers four sub-steps.  Stage kt+2's
+        // loads go into stage kt's slot from the barrier at the end of stage
+        // kt on (every wave has finished reading the slot): a third under
+        // stage kt's last sub-step, the rest under stage kt+1's first two, so
+        // the CU's address unit (one 1 KiB load takes it ~16 cycles) is never
+        // asked for more than three quarters of a sub-step and each load has
+        // at least a sub-step to land.  Stage kt+1's first fragments are read
+        // under stage kt's last MFMAs.  Each sub-step's fragment reads and
+        // loads are written interleaved (op_is_load) and scheduled one per
+        // MFMA (sched_ops).  Iterations whose loads all fall on whole stages
+        // take the stage offset in the loads' scalar operand and skip the
+        // per-lane tail checks.
         static_assert(SUB == 4 && NS == 2, "four sub-steps run with a two-stage ring");
-        for (int kt = 0; kt < KT; ++kt) {
+        constexpr int NM = TM * TN, NR = TM + TN;
+        constexpr int SPAN = NM * 7 / 8;
+        auto kstep = [&](int kt, auto whole) {
+            constexpr bool WHOLE = decltype(whole)::value;
+            // Fragment reads of sub-step ss into `set`, with loads
+            // [first, first + NL) of stage st into `slot` among them.
+            auto ops = [&](const uint8_t *src, int ss, int set, auto nl, int st, int slot,
+                           int first) {
+                constexpr int NL = decltype(nl)::value;
+                const int sl = ((2 * ss + lhalf) ^ swz) << 4;
+                int l = first;
+#pragma unroll
+                for (int r = 0; r < NR; ++r) {
+                    if (r < TM)
+                        af[set][r] = *(const v4i *)(src + a_row_off[r] + sl);
+                    else
+                        bf[set][r - TM] = *(const v4i *)(src + b_row_off[r - TM] + sl);
+                    if ((r + 1) * NL / NR != r * NL / NR) {
+                        if constexpr (WHOLE)
+                            issue_whole(st, slot, l, 1);
+                        else
+                            issue_stage(st, slot, l, 1);
+                        ++l;
+                    }
+                }
+            };
+            using L0 = std::integral_constant<int, P0>;
+            using L1 = std::integral_constant<int, P1>;
+            using L2 = std::integral_constant<int, P2>;
+            using LN = std::integral_constant<int, 0>;
             const uint8_t *s = smem + (kt & 1) * STAGE;
             const int nslot = (kt + 1) & 1;
-            read_frags(s, 1, 1);
             mfmas(0);
-            issue_stage(kt + 1, nslot, 0, H0);
-#pragma unroll
-            for (int i = 0; i < TM * TN; ++i) {
-                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-                if (i < TM + TN) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-                if (i >= TM * TN - H0) __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
-            }
-            read_frags(s, 2, 0);
+            ops(s, 1, 1, L1{}, kt + 1, nslot, P0);
+            sched_ops<NM, NR, P1, SPAN>();
             mfmas(1);
-            issue_stage(kt + 1, nslot, H0, H1);
-#pragma unroll
-            for (int i = 0; i < TM * TN; ++i) {
-                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-                if (i < TM + TN) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-                if (i >= TM * TN - H1) __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
-            }
-            read_frags(s, 3, 1);
+            ops(s, 2, 0, L2{}, kt + 1, nslot, P0 + P1);
+            sched_ops<NM, NR, P2, SPAN>();
             mfmas(0);
-#pragma unroll
-            for (int i = 0; i < TM * TN; ++i) {
-                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-                if (i < TM + TN) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-            }
+            ops(s, 3, 1, LN{}, kt + 1, nslot, NIW);
+            sched_ops<NM, NR, 0, SPAN>();
 #pragma unroll
             for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[0][i]));
 #pragma unroll
@@ -458,14 +567,16 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
             for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[1][i]));
 #pragma unroll
             for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bf[1][j]));
-            read_frags(smem + nslot * STAGE, 0, 0);
             mfmas(1);
-#pragma unroll
-            for (int i = 0; i < TM * TN; ++i) {
-                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-                if (i < TM + TN) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-            }
-        }
+            ops(smem + nslot * STAGE, 0, 0, L0{}, kt + 2, kt & 1, 0);
+            sched_ops<NM, NR, P0, SPAN>();
+        };
+        // Iteration kt issues stages kt+1 and kt+2.
+        const int ktw = (int)(kbytes / BK);  // whole stages
+        const int kt_whole = soff_ok ? (ktw - 2 < KT ? (ktw - 2 > 0 ? ktw - 2 : 0) : KT) : 0;
+        int kt = 0;
+        for (; kt < kt_whole; ++kt) kstep(kt, std::true_type{});
+        for (; kt < KT; ++kt) kstep(kt, std::false_type{});
     }
 
     // Staged epilogue.  The MFMAs take B^T's fragment as their first operand,
