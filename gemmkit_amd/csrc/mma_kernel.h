@@ -465,41 +465,65 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     stage_barrier();
     read_frags(smem, 0, 0);
 
+    // Fragment reads of sub-step ss into `set`, with loads [first, first + NL)
+    // of stage st into `slot` among them in program order (op_is_load); whole
+    // stages take the scalar-offset loads.
+    constexpr int NM = TM * TN, NR = TM + TN;
+    constexpr int SPAN = NM * 7 / 8;
+    auto ops = [&](auto whole, const uint8_t *src, int ss, int set, auto nl, int st, int slot,
+                   int first) {
+        constexpr bool WHOLE = decltype(whole)::value;
+        constexpr int NL = decltype(nl)::value;
+        const int sl = ((2 * ss + lhalf) ^ swz) << 4;
+        int l = first;
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            if (r < TM)
+                af[set][r] = *(const v4i *)(src + a_row_off[r] + sl);
+            else
+                bf[set][r - TM] = *(const v4i *)(src + b_row_off[r - TM] + sl);
+            if ((r + 1) * NL / NR != r * NL / NR) {
+                if constexpr (WHOLE)
+                    issue_whole(st, slot, l, 1);
+                else
+                    issue_stage(st, slot, l, 1);
+                ++l;
+            }
+        }
+    };
+    const int ktw = (int)(kbytes / BK);  // whole stages
+
     if constexpr (SUB == 2) {
-        for (int kt = 0; kt < KT; ++kt) {
+        using LA = std::integral_constant<int, H0>;
+        using LC = std::integral_constant<int, H1>;
+        auto kstep = [&](int kt, auto whole) {
             const uint8_t *s = smem + (kt % NS) * STAGE;
             const int nslot = (kt + NS - 1) % NS;
-            read_frags(s, 1, 1);
             mfmas(0);
-            issue_stage(kt + NS - 1, nslot, 0, H0);
-    #pragma unroll
-            for (int i = 0; i < TM * TN; ++i) {
-                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-                if (i < TM + TN) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-                if (i >= TM * TN - H0) __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
-            }
-    #pragma unroll
+            ops(whole, s, 1, 1, LA{}, kt + NS - 1, nslot, 0);
+            sched_ops<NM, NR, H0, SPAN>();
+#pragma unroll
             for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[0][i]));
-    #pragma unroll
+#pragma unroll
             for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bf[0][j]));
             // Stage kt+1's loads were issued at iteration kt+2-NS; issued after
             // them: NS-3 whole iterations plus this phase A.
             wait_vmcnt<(NS - 3) * NIW + H0>();
             stage_barrier();
-    #pragma unroll
+#pragma unroll
             for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[1][i]));
-    #pragma unroll
+#pragma unroll
             for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bf[1][j]));
-            read_frags(smem + ((kt + 1) % NS) * STAGE, 0, 0);
             mfmas(1);
-            issue_stage(kt + NS - 1, nslot, H0, H1);
-    #pragma unroll
-            for (int i = 0; i < TM * TN; ++i) {
-                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-                if (i < TM + TN) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-                if (i >= TM * TN - H1) __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
-            }
-        }
+            ops(whole, smem + ((kt + 1) % NS) * STAGE, 0, 0, LC{}, kt + NS - 1, nslot, H0);
+            sched_ops<NM, NR, H1, SPAN>();
+        };
+        // Iteration kt issues stage kt+NS-1.
+        const int lim = ktw - NS + 1;
+        const int kt_whole = soff_ok ? (lim < KT ? (lim > 0 ? lim : 0) : KT) : 0;
+        int kt = 0;
+        for (; kt < kt_whole; ++kt) kstep(kt, std::true_type{});
+        for (; kt < KT; ++kt) kstep(kt, std::false_type{});
     } else {
         // 128-byte stages in a two-stage ring: each row of a stage is one
         // whole 128-byte line of K (half the cache-line requests of two
@@ -516,32 +540,7 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
         // take the stage offset in the loads' scalar operand and skip the
         // per-lane tail checks.
         static_assert(SUB == 4 && NS == 2, "four sub-steps run with a two-stage ring");
-        constexpr int NM = TM * TN, NR = TM + TN;
-        constexpr int SPAN = NM * 7 / 8;
         auto kstep = [&](int kt, auto whole) {
-            constexpr bool WHOLE = decltype(whole)::value;
-            // Fragment reads of sub-step ss into `set`, with loads
-            // [first, first + NL) of stage st into `slot` among them.
-            auto ops = [&](const uint8_t *src, int ss, int set, auto nl, int st, int slot,
-                           int first) {
-                constexpr int NL = decltype(nl)::value;
-                const int sl = ((2 * ss + lhalf) ^ swz) << 4;
-                int l = first;
-#pragma unroll
-                for (int r = 0; r < NR; ++r) {
-                    if (r < TM)
-                        af[set][r] = *(const v4i *)(src + a_row_off[r] + sl);
-                    else
-                        bf[set][r - TM] = *(const v4i *)(src + b_row_off[r - TM] + sl);
-                    if ((r + 1) * NL / NR != r * NL / NR) {
-                        if constexpr (WHOLE)
-                            issue_whole(st, slot, l, 1);
-                        else
-                            issue_stage(st, slot, l, 1);
-                        ++l;
-                    }
-                }
-            };
             using L0 = std::integral_constant<int, P0>;
             using L1 = std::integral_constant<int, P1>;
             using L2 = std::integral_constant<int, P2>;
@@ -549,13 +548,13 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
             const uint8_t *s = smem + (kt & 1) * STAGE;
             const int nslot = (kt + 1) & 1;
             mfmas(0);
-            ops(s, 1, 1, L1{}, kt + 1, nslot, P0);
+            ops(whole, s, 1, 1, L1{}, kt + 1, nslot, P0);
             sched_ops<NM, NR, P1, SPAN>();
             mfmas(1);
-            ops(s, 2, 0, L2{}, kt + 1, nslot, P0 + P1);
+            ops(whole, s, 2, 0, L2{}, kt + 1, nslot, P0 + P1);
             sched_ops<NM, NR, P2, SPAN>();
             mfmas(0);
-            ops(s, 3, 1, LN{}, kt + 1, nslot, NIW);
+            ops(whole, s, 3, 1, LN{}, kt + 1, nslot, NIW);
             sched_ops<NM, NR, 0, SPAN>();
 #pragma unroll
             for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[0][i]));
@@ -568,11 +567,10 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
 #pragma unroll
             for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bf[1][j]));
             mfmas(1);
-            ops(smem + nslot * STAGE, 0, 0, L0{}, kt + 2, kt & 1, 0);
+            ops(whole, smem + nslot * STAGE, 0, 0, L0{}, kt + 2, kt & 1, 0);
             sched_ops<NM, NR, P0, SPAN>();
         };
         // Iteration kt issues stages kt+1 and kt+2.
-        const int ktw = (int)(kbytes / BK);  // whole stages
         const int kt_whole = soff_ok ? (ktw - 2 < KT ? (ktw - 2 > 0 ? ktw - 2 : 0) : KT) : 0;
         int kt = 0;
         for (; kt < kt_whole; ++kt) kstep(kt, std::true_type{});
