@@ -8,11 +8,11 @@ Maintenance tool, not part of the library's call path.  On a GPU box:
 
 ``--measure`` times every shape with each tile forced (GEMMKIT_HIP_TILE) and
 with the library's own choice ("auto"), one HIP-graph replay of 12 calls per
-point.  ``--fit`` fits per-tile efficiencies, epilogue overlap and speed,
-per-output-kind epilogue costs, the per-tile latency and the f32 rate by
-least squares on log time, then refines them to minimise the regret of the
-picks (time of the predicted best tile over the measured best), and prints
-the constants and each shape's pick.
+point.  ``--fit`` fits per-tile efficiencies (with a factor for int8 inputs),
+epilogue overlap, epilogue speeds (plain and requantizing), per-output-kind
+epilogue costs, the per-tile latency and the f32 rate by least squares on log
+time, then refines them to minimise the regret of the picks (time of the
+predicted best tile over the measured best), and prints the constants and each shape's pick.
 """
 from __future__ import annotations
 
@@ -141,19 +141,22 @@ def fit(path: str) -> None:
         hd = dict(zip(tn, p[i:i + nt])); i += nt
         ce = dict(zip(KINDS, p[i:i + 4])); i += 4
         lat, rf, s = p[i], p[i + 1], p[i + 2]; i += 3
-        es = dict(zip(tn, [1.0] + list(p[i:i + nt - 1])))
-        return e1, e2, hd, ce, lat, rf, s, es
+        es = dict(zip(tn, [1.0] + list(p[i:i + nt - 1]))); i += nt - 1
+        eq = dict(zip(tn, [1.0] + list(p[i:i + nt - 1]))); i += nt - 1
+        ei = dict(zip(tn, [1.0] + list(p[i:i + nt - 1])))
+        return e1, e2, hd, ce, lat, rf, s, es, eq, ei
 
     def model(p, meta, t):
-        e1, e2, hd, ce, lat, rf, s, es = unpack(p)
+        e1, e2, hd, ce, lat, rf, s, es, eq, ei = unpack(p)
         bm, bn, occ = TILES[t]
         ntile = -(-meta["M"] // bm) * -(-meta["N"] // bn) * meta["batch"]
         per = -(-ntile // CUS)
-        eff = e1[t] if min(per, occ) == 1 else e2[t]
+        eff = (e1[t] if min(per, occ) == 1 else e2[t]) * (ei[t] if meta["kind"] in ("i32", "q8") else 1.0)
         area = bm * bn
         kf = max(meta["K"], 64) / 4096.0 * (rf if meta.get("f32_in") else 1.0)
         exposed = per - hd[t] * (per - 1)
-        return s * (per * area * kf / eff + (area * ce[meta["kind"]] * es[t] + lat) * exposed)
+        speed = eq[t] if meta["kind"] == "q8" else es[t]
+        return s * (per * area * kf / eff + (area * ce[meta["kind"]] * speed + lat) * exposed)
 
     def resid(p):
         return [np.log(model(p, m, t) / us) for m, t, us in pts]
@@ -174,9 +177,11 @@ def fit(path: str) -> None:
         return tot
 
     p0 = [0.7] * nt + [0.5] * len(occ2) + [0.5] * nt + [0.3, 0.5, 0.3, 0.2, 4000, 4, 0.0005] + \
-        [1.0] * (nt - 1)
-    lo = [0.05] * (nt + len(occ2)) + [0.0] * nt + [0.0] * 4 + [0, 1, 1e-5] + [0.2] * (nt - 1)
-    hi = [1.0] * (nt + len(occ2)) + [1.0] * nt + [3.0] * 4 + [50000, 30, 1e-2] + [3.0] * (nt - 1)
+        [1.0] * (3 * nt - 3)
+    lo = [0.05] * (nt + len(occ2)) + [0.0] * nt + [0.0] * 4 + [0, 1, 1e-5] + [0.2] * (2 * nt - 2) + \
+        [0.7] * (nt - 1)
+    hi = [1.0] * (nt + len(occ2)) + [1.0] * nt + [3.0] * 4 + [50000, 30, 1e-2] + [3.0] * (2 * nt - 2) + \
+        [1.3] * (nt - 1)
     start = least_squares(resid, p0, bounds=(lo, hi)).x
     obj = lambda p: regret(p) + 0.2 * np.sqrt(np.mean(np.square(resid(p))))  # noqa: E731
     best, bo = start, obj(start)
@@ -192,13 +197,15 @@ def fit(path: str) -> None:
                 cur, co = q, o
         if co < bo:
             best, bo = cur, co
-    e1, e2, hd, ce, lat, rf, s, es = unpack(best)
-    print("eff (one tile / two sharing a CU):", {t: (round(e1[t], 6), round(e2.get(t, e1[t]), 6))
-                                                for t in tn})
-    print("hide:", {t: round(hd[t], 6) for t in tn})
-    print("epilogue speed:", {t: round(es[t], 6) for t in tn})
-    print("c_epi:", {k: round(v, 6) for k, v in ce.items()}, "latency", round(lat, 3),
-          "f32 rate", round(rf, 6))
+    e1, e2, hd, ce, lat, rf, s, es, eq, ei = unpack(best)
+    r6 = lambda x: round(float(x), 6)  # noqa: E731
+    print("eff (one tile / two sharing a CU):", {t: (r6(e1[t]), r6(e2.get(t, e1[t]))) for t in tn})
+    print("hide:", {t: r6(hd[t]) for t in tn})
+    print("epilogue speed:", {t: r6(es[t]) for t in tn})
+    print("requantizing epilogue speed:", {t: r6(eq[t]) for t in tn})
+    print("i8 efficiency factor:", {t: r6(ei[t]) for t in tn})
+    print("c_epi:", {k: r6(v) for k, v in ce.items()}, "latency", round(float(lat), 3),
+          "f32 rate", r6(rf))
     print("regret", round(regret(best), 4), "rms log error",
           round(float(np.sqrt(np.mean(np.square(resid(best))))), 4))
     for name, d in data.items():

@@ -336,38 +336,40 @@ bool skinny_enabled() {
 
 // Tile choice: the tile with the smallest makespan.  Tiles spread evenly over
 // the CUs, so the busiest CU runs per_cu = ceil(tiles / CUs) of them, up to
-// `occ` at a time.  A tile costs its main loop, BM*BN*kf / eff[n-1] (kf: K
-// bytes per row relative to 4096, times the f32 matrix cores' lower rate for
-// f32 inputs; n tiles sharing a CU deliver eff[n-1] of its matrix-core peak),
-// plus its epilogue, BM*BN * c_epi(output kind) * epi (the tile's epilogue
-// speed: eight waves per CU finish it sooner), plus a fixed per-tile latency
-// (first stages in flight).  A fraction `hide` of the epilogue and latency
-// overlaps the next tile's main loop when a CU runs more than one; the last
-// is never hidden.  The constants are the fit of gemmkit_amd/calibrate_tiles.py
-// to graph-timed runs of 13 shapes x 8 tiles (int8 i32 and requantized, bf16
-// with f32 and bf16 output, batched attention scores, f32; 1024^2 to 4096^3
-// and 2048 x 11008 x 4096): least squares on log time, then refined so the
-// chosen tile is within noise of the best measured one on each shape.
+// `occ` at a time.  A tile costs its main loop, BM*BN*kf / eff (kf: K bytes
+// per row relative to 4096, times the f32 matrix cores' lower rate for f32
+// inputs; eff[n-1] is the share of the CU's matrix-core peak n tiles sharing
+// it deliver, times eff_i8 for int8 inputs, whose main loop draws more power
+// per byte), plus its epilogue, BM*BN * c_epi(output kind) * epi (the tile's
+// epilogue speed, epi_q8 for the requantizing one: eight waves per CU finish
+// the arithmetic sooner), plus a fixed per-tile latency (first stages in
+// flight).  A fraction `hide` of the epilogue and latency overlaps the next
+// tile's main loop when a CU runs more than one; the last is never hidden.
+// The constants are the fit of gemmkit_amd/calibrate_tiles.py to graph-timed
+// runs of 13 shapes x 8 tiles (int8 i32 and requantized, bf16 with f32 and
+// bf16 output, batched attention scores, f32; 1024^2 to 4096^3 and
+// 2048 x 11008 x 4096): least squares on log time, then refined so the chosen
+// tile is the best measured one on each shape.
 Tile pick_tile(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind kind, InType in) {
     bool forced;
     Tile t = env_tile(&forced);
     if (forced) return t;
-    struct Cand { Tile t; int bm, bn, occ; double eff[2], hide, epi; };
+    struct Cand { Tile t; int bm, bn, occ; double eff[2], eff_i8, hide, epi, epi_q8; };
     static const Cand cands[] = {
-        {Tile::T256x256, 256, 256, 1, {0.881972, 0.881972}, 0.408704, 1.0},
-        {Tile::T256x256w8, 256, 256, 1, {1.0, 1.0}, 0.435266, 0.870287},
-        {Tile::T256x128o2, 256, 128, 2, {0.771698, 0.648456}, 0.751995, 0.804527},
-        {Tile::T256x128, 256, 128, 1, {0.710394, 0.710394}, 0.502005, 0.636165},
-        {Tile::T128x128, 128, 128, 2, {0.818596, 0.571382}, 0.885997, 0.2},
-        {Tile::T64x64, 64, 64, 2, {0.817629, 0.413534}, 0.926261, 3.0},
-        {Tile::T256x256k128, 256, 256, 1, {0.840252, 0.840252}, 0.361402, 0.901789},
-        {Tile::T256x256w8k128, 256, 256, 1, {1.0, 1.0}, 0.342395, 0.847936},
+        {Tile::T256x256, 256, 256, 1, {0.876049, 0.876049}, 1.0, 0.446527, 1.0, 1.0},
+        {Tile::T256x256w8, 256, 256, 1, {0.905052, 0.905052}, 1.3, 0.397345, 1.141787, 0.935765},
+        {Tile::T256x128o2, 256, 128, 2, {0.773415, 0.583568}, 1.11073, 0.615115, 0.420867, 0.565076},
+        {Tile::T256x128, 256, 128, 1, {0.726001, 0.726001}, 1.064577, 0.208026, 0.311532, 0.901659},
+        {Tile::T128x128, 128, 128, 2, {0.787324, 0.532058}, 1.076563, 0.845232, 0.26268, 0.2},
+        {Tile::T64x64, 64, 64, 2, {0.814864, 0.441999}, 0.815275, 0.925765, 3.0, 2.140505},
+        {Tile::T256x256k128, 256, 256, 1, {0.891258, 0.891258}, 1.3, 0.327803, 1.0266, 1.143453},
+        {Tile::T256x256w8k128, 256, 256, 1, {0.907065, 0.907065}, 1.257551, 0.383056, 1.010608, 0.804656},
     };
-    const double c_epi = kind == EpiKind::Q8 ? 0.354519
-                         : kind == EpiKind::I32 ? 0.344598
-                         : kind == EpiKind::F32 ? 0.1222 : 0.063011;
-    constexpr double kTileLatency = 21811.149;  // in the units of area / eff
-    constexpr double kF32Rate = 4.823842;    // f32 main-loop cost per K byte vs i8/bf16
+    const double c_epi = kind == EpiKind::Q8 ? 0.750473
+                         : kind == EpiKind::I32 ? 0.376841
+                         : kind == EpiKind::F32 ? 0.153472 : 0.0;
+    constexpr double kTileLatency = 19011.223;  // in the units of area / eff
+    constexpr double kF32Rate = 4.54331;    // f32 main-loop cost per K byte vs i8/bf16
     const double kf = (double)std::max<int64_t>(kbytes, 64) / 4096.0 *
                       (in == InType::F32 ? kF32Rate : 1.0);
     double best = 1e300;
@@ -379,8 +381,9 @@ Tile pick_tile(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind kind
         const int together = (int)std::min<int64_t>(per_cu, c.occ);
         const double area = (double)c.bm * c.bn;
         const double exposed = per_cu - c.hide * (per_cu - 1);
-        const double cost = per_cu * area * kf / c.eff[together - 1] +
-                            (area * c_epi * c.epi + kTileLatency) * exposed;
+        const double eff = c.eff[together - 1] * (in == InType::I8 ? c.eff_i8 : 1.0);
+        const double epi = kind == EpiKind::Q8 ? c.epi_q8 : c.epi;
+        const double cost = per_cu * area * kf / eff + (area * c_epi * epi + kTileLatency) * exposed;
         if (cost < best * 0.999) { best = cost; bt = c.t; }
     }
     return bt;
