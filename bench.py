@@ -8,7 +8,10 @@ xorshift* stream, resident in HBM before timing.  A "step" is one gemm_i8 call
 through the C ABI.  The timed region replays a HIP graph holding the K calls
 (captured from the same C-ABI calls on the launch stream), so host-side call
 overhead does not hide behind or inflate the kernel time; HIP events on that
-stream bracket it, with a device synchronize on both sides.
+stream bracket it, with a device synchronize on both sides.  Before that,
+untimed warmup calls run for at least --warmup calls and --warmup-ms of wall
+time (300 ms by default): from idle the GPU takes some 100 ms of load to raise
+its clocks, and a shorter warmup times the ramp instead of the steady state.
 
 The other workloads of the path follow under "workloads": the requantizing
 int8 linear layer with a prepacked weight (2048 x 4096 x 11008, 16 calls per
@@ -45,6 +48,9 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--warmup-ms", type=float, default=300.0,
+                   help="keep issuing untimed warmup calls until this much time has passed "
+                        "(the GPU raises its clocks only after some 100 ms of load)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extra", action="store_true", help="headline workload only")
     p.add_argument("--only", default=None, help="run one workload by name (profiling)")
@@ -56,15 +62,24 @@ class Timer:
     """Times `steps` calls of `fn` (a list of callables cycled in order) on the
     current stream: captured into a HIP graph and replayed, or eager."""
 
-    def __init__(self, eager: bool):
+    def __init__(self, eager: bool, warmup_ms: float):
         self.eager = eager
+        self.warmup_ms = warmup_ms
 
     def __call__(self, fns, steps: int, warmup: int) -> float:
         import torch
         if callable(fns):
             fns = [fns]
-        for i in range(max(warmup, len(fns))):
+        # Untimed warmup: at least `warmup` calls, and at least warmup_ms of
+        # wall time with the device kept busy (synchronizing every 32 calls
+        # so the host does not run ahead of it).
+        t0 = time.perf_counter()
+        i = 0
+        while i < max(warmup, len(fns)) or (time.perf_counter() - t0) * 1e3 < self.warmup_ms:
             fns[i % len(fns)]()
+            i += 1
+            if i % 32 == 0:
+                torch.cuda.synchronize()
         torch.cuda.synchronize()
         stream = torch.cuda.current_stream()
         start = torch.cuda.Event(enable_timing=True)
@@ -107,7 +122,7 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     gk.set_synchronous(False)
-    timed = Timer(args.eager)
+    timed = Timer(args.eager, args.warmup_ms)
     props = torch.cuda.get_device_properties(0)
     workloads = {}
 
@@ -165,6 +180,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_ms_min": args.warmup_ms,
         "ms_per_step": i8_ms,
         "higher_is_better": True,
         "scaling": "weak",

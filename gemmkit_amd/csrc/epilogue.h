@@ -22,11 +22,21 @@
 
 namespace gk {
 
+// f32 -> bf16 as gemmkit's narrowing (half::bf16::from_f32): round to nearest
+// even, NaN kept quiet with its sign and top payload bits ((bits >> 16) |
+// 0x40).  gfx950's v_cvt_pk_bf16_f32 gives exactly that for every f32 input
+// (denormals preserved, the kernels' default float mode) and converts two
+// values per instruction.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t bf16x2_rne(float lo, float hi) {
+    const f32x2_t v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
 __device__ __forceinline__ uint16_t bf16_rne(float f) {
-    uint32_t bits = __float_as_uint(f);
-    if ((bits & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((bits >> 16) | 0x0040u);
-    uint32_t lsb = (bits >> 16) & 1u;
-    return (uint16_t)((bits + 0x7FFFu + lsb) >> 16);
+    return (uint16_t)bf16x2_rne(f, 0.0f);
 }
 
 __device__ __forceinline__ float bf16_widen(uint16_t h) {
@@ -222,9 +232,9 @@ __device__ __forceinline__ void store4(const EpiParams &ep, int64_t z, int row, 
             for (int e = 0; e < 4; ++e) f[e] = fused_apply(ep, f[e], fb[e]);
         }
         v2u_e o;
-        o[0] = (uint32_t)bf16_rne(f[0]) | ((uint32_t)bf16_rne(f[1]) << 16);
-        o[1] = (uint32_t)bf16_rne(f[2]) | ((uint32_t)bf16_rne(f[3]) << 16);
-        *c = o;
+        o[0] = bf16x2_rne(f[0], f[1]);
+        o[1] = bf16x2_rne(f[2], f[3]);
+        __builtin_nontemporal_store(o, c);
     } else {
         const uint32_t word = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
                               ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)q[3] << 24);

@@ -124,6 +124,39 @@ def test_bf16_out(dev, m, k, n):
     assert (np.abs(got - ref) <= 2.0 ** -8 * np.maximum(np.abs(ref), floor) * 1.01).all()
 
 
+@pytest.mark.parametrize("m,n", [(512, 512), (512, 8), (1, 512)])
+@pytest.mark.parametrize("alpha", [1.0, 0.3])
+def test_bf16_out_rounding_bit_exact(dev, m, n, alpha):
+    """One nonzero product per output (k = 8, a single nonzero column of A and
+    row of B), so the f32 value before narrowing is known exactly:
+    f32(alpha * a_i * b_j), alpha being a bf16 scalar like the operands
+    (gemm::<bf16> takes alpha: bf16).  Its bf16 bits must equal the oracle's
+    RNE with gemmkit's NaN rule, ties included (products of two bf16 carry up
+    to 16 significant bits)."""
+    k = 8
+    rng = np.random.default_rng(7 + m + n)
+
+    def bf16_vals(cnt):
+        mant = rng.integers(0, 128, cnt)
+        expo = rng.integers(-20, 21, cnt)
+        sign = rng.choice([-1.0, 1.0], cnt)
+        return (sign * (1.0 + mant / 128.0) * np.exp2(expo)).astype(np.float32)
+
+    av, bv = bf16_vals(m), bf16_vals(n)
+    a = np.zeros((m, k), np.float32)
+    b = np.zeros((k, n), np.float32)
+    a[:, 3], b[3, :] = av, bv
+    alpha_bf = oracle.bf16_to_f32(oracle.bf16_bits(np.array([alpha], np.float32)))[0]
+    want = oracle.bf16_bits(alpha_bf * (av[:, None] * bv[None, :]).astype(np.float32))
+    cd = bf16_tensor_from_bits(np.zeros(m * n, np.uint16), dev)
+    gk.gemm(alpha, gk.MatRef.from_row_major(bf16_tensor_from_bits(oracle.bf16_bits(a), dev), m, k),
+            gk.MatRef.from_row_major(bf16_tensor_from_bits(oracle.bf16_bits(b), dev), k, n), 0.0,
+            gk.MatMut.from_row_major(cd, m, n))
+    import torch
+    got = cd.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, want.reshape(-1))
+
+
 def test_batched_bf16_attention_scores(dev):
     """Batched bf16 x bf16 -> f32, the attention-score shape at full size:
     64 x (512 x 128) . (128 x 512) with B = K^T via strides, alpha = 1/sqrt(128).
