@@ -90,6 +90,23 @@ def version() -> str:
     return _lib.lib().gk_version().decode()
 
 
+TILE_NAMES = {0: "256x256", 1: "256x128", 2: "128x128", 3: "64x64", 4: "256x256w8",
+              5: "256x128o2", 6: "256x256k128", 7: "256x256w8k128"}
+_IN_CODES = {"i8": 0, "bf16": 1, "f32": 2}
+_KIND_CODES = {"i32": 0, "f32": 1, "bf16": 2, "q8": 3}
+
+
+def debug_plan(in_type: str, kind: str, m: int, n: int, kbytes: int, batch: int = 1):
+    """Extension (no reference counterpart): the matrix-core launch plan the
+    dispatcher would choose for an m x n product in the kernel frame with
+    `kbytes` bytes of K per row, as (tile, na, tile_b): na > 0 means a second
+    launch covers columns [na, n) with tile_b.  Host-only."""
+    t, na, tb = C.c_int32(), C.c_int64(), C.c_int32()
+    _check(_lib.lib().gk_debug_plan(_IN_CODES[in_type], _KIND_CODES[kind], m, n, batch, kbytes,
+                                    C.byref(t), C.byref(na), C.byref(tb)))
+    return TILE_NAMES[t.value], na.value, TILE_NAMES[tb.value]
+
+
 def set_synchronous(on: bool) -> None:
     """True (default): every call waits for its kernels, like the reference."""
     _lib.lib().gk_set_synchronous(1 if on else 0)

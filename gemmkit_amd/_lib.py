@@ -55,6 +55,9 @@ _BIAS = C.POINTER(BiasC)
 SIGNATURES: dict[str, tuple] = {
     "gk_last_error": (C.c_char_p, []),
     "gk_version": (C.c_char_p, []),
+    "gk_debug_plan": (C.c_int, [C.c_int32, C.c_int32, C.c_int64, C.c_int64, C.c_int64, C.c_int64,
+                                C.POINTER(C.c_int32), C.POINTER(C.c_int64),
+                                C.POINTER(C.c_int32)]),
     "gk_init": (C.c_int, []),
     "gk_set_stream": (C.c_int, [_vp]),
     "gk_get_stream": (_vp, []),

@@ -350,21 +350,22 @@ bool skinny_enabled() {
 // bf16 output, batched attention scores, f32; 1024^2 to 4096^3 and
 // 2048 x 11008 x 4096): least squares on log time, then refined so the chosen
 // tile is the best measured one on each shape.
-Tile pick_tile(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind kind, InType in) {
-    bool forced;
-    Tile t = env_tile(&forced);
-    if (forced) return t;
-    struct Cand { Tile t; int bm, bn, occ; double eff[2], eff_i8, hide, epi, epi_q8; };
-    static const Cand cands[] = {
-        {Tile::T256x256, 256, 256, 1, {0.876049, 0.876049}, 1.0, 0.446527, 1.0, 1.0},
-        {Tile::T256x256w8, 256, 256, 1, {0.905052, 0.905052}, 1.3, 0.397345, 1.141787, 0.935765},
-        {Tile::T256x128o2, 256, 128, 2, {0.773415, 0.583568}, 1.11073, 0.615115, 0.420867, 0.565076},
-        {Tile::T256x128, 256, 128, 1, {0.726001, 0.726001}, 1.064577, 0.208026, 0.311532, 0.901659},
-        {Tile::T128x128, 128, 128, 2, {0.787324, 0.532058}, 1.076563, 0.845232, 0.26268, 0.2},
-        {Tile::T64x64, 64, 64, 2, {0.814864, 0.441999}, 0.815275, 0.925765, 3.0, 2.140505},
-        {Tile::T256x256k128, 256, 256, 1, {0.891258, 0.891258}, 1.3, 0.327803, 1.0266, 1.143453},
-        {Tile::T256x256w8k128, 256, 256, 1, {0.907065, 0.907065}, 1.257551, 0.383056, 1.010608, 0.804656},
-    };
+struct TileCand { Tile t; int bm, bn, occ; double eff[2], eff_i8, hide, epi, epi_q8; };
+static const TileCand kTileCands[] = {
+    {Tile::T256x256, 256, 256, 1, {0.876049, 0.876049}, 1.0, 0.446527, 1.0, 1.0},
+    {Tile::T256x256w8, 256, 256, 1, {0.905052, 0.905052}, 1.3, 0.397345, 1.141787, 0.935765},
+    {Tile::T256x128o2, 256, 128, 2, {0.773415, 0.583568}, 1.11073, 0.615115, 0.420867, 0.565076},
+    {Tile::T256x128, 256, 128, 1, {0.726001, 0.726001}, 1.064577, 0.208026, 0.311532, 0.901659},
+    {Tile::T128x128, 128, 128, 2, {0.787324, 0.532058}, 1.076563, 0.845232, 0.26268, 0.2},
+    {Tile::T64x64, 64, 64, 2, {0.814864, 0.441999}, 0.815275, 0.925765, 3.0, 2.140505},
+    {Tile::T256x256k128, 256, 256, 1, {0.891258, 0.891258}, 1.3, 0.327803, 1.0266, 1.143453},
+    {Tile::T256x256w8k128, 256, 256, 1, {0.907065, 0.907065}, 1.257551, 0.383056, 1.010608, 0.804656},
+};
+
+// Model cost of running an M x N (x batch) product with tile c, in the units
+// of area / eff.
+double tile_cost(const TileCand &c, int64_t M, int64_t N, int64_t batch, int64_t kbytes,
+                 EpiKind kind, InType in) {
     const double c_epi = kind == EpiKind::Q8 ? 0.750473
                          : kind == EpiKind::I32 ? 0.376841
                          : kind == EpiKind::F32 ? 0.153472 : 0.0;
@@ -372,21 +373,77 @@ Tile pick_tile(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind kind
     constexpr double kF32Rate = 4.54331;    // f32 main-loop cost per K byte vs i8/bf16
     const double kf = (double)std::max<int64_t>(kbytes, 64) / 4096.0 *
                       (in == InType::F32 ? kF32Rate : 1.0);
+    const int64_t cus = g_num_cus > 0 ? g_num_cus : 256;
+    const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * batch;
+    const int64_t per_cu = (tiles + cus - 1) / cus;
+    const int together = (int)std::min<int64_t>(per_cu, c.occ);
+    const double area = (double)c.bm * c.bn;
+    const double exposed = per_cu - c.hide * (per_cu - 1);
+    const double eff = c.eff[together - 1] * (in == InType::I8 ? c.eff_i8 : 1.0);
+    const double epi = kind == EpiKind::Q8 ? c.epi_q8 : c.epi;
+    return per_cu * area * kf / eff + (area * c_epi * epi + kTileLatency) * exposed;
+}
+
+const TileCand &tile_cand(Tile t) {
+    for (const TileCand &c : kTileCands)
+        if (c.t == t) return c;
+    return kTileCands[0];
+}
+
+Tile pick_tile(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind kind, InType in,
+               double *cost_out = nullptr) {
+    bool forced;
+    Tile t = env_tile(&forced);
+    if (forced) return t;
     double best = 1e300;
     Tile bt = Tile::T64x64;
-    const int64_t cus = g_num_cus > 0 ? g_num_cus : 256;
-    for (const Cand &c : cands) {
-        const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * batch;
-        const int64_t per_cu = (tiles + cus - 1) / cus;
-        const int together = (int)std::min<int64_t>(per_cu, c.occ);
-        const double area = (double)c.bm * c.bn;
-        const double exposed = per_cu - c.hide * (per_cu - 1);
-        const double eff = c.eff[together - 1] * (in == InType::I8 ? c.eff_i8 : 1.0);
-        const double epi = kind == EpiKind::Q8 ? c.epi_q8 : c.epi;
-        const double cost = per_cu * area * kf / eff + (area * c_epi * epi + kTileLatency) * exposed;
+    for (const TileCand &c : kTileCands) {
+        const double cost = tile_cost(c, M, N, batch, kbytes, kind, in);
         if (cost < best * 0.999) { best = cost; bt = c.t; }
     }
+    if (cost_out) *cost_out = best;
     return bt;
+}
+
+// Tail split.  When a product's tiles take two or more rounds of the CUs and
+// the last round is short, most CUs idle through it.  Cutting the kernel
+// frame's N so that the first part fills the full rounds exactly and running
+// the rest as a second launch with a 128-wide tile (twice the tiles, each
+// half the work) shortens that last round.  The model decides: the split is
+// taken when the two parts' modelled cost, plus one launch, beats the single
+// launch.  Only the 128-wide tiles are candidates for the rest (the model's
+// efficiencies are fitted on full rounds; among those two it ranks the
+// measured 2048 x 2816 x 4096 rests correctly).  Outputs do not change: every
+// element's K order is the same in all tiles.  GEMMKIT_HIP_TAILSPLIT=0 turns
+// it off.
+struct TailSplit { int64_t na; Tile ta, tb; };
+constexpr double kLaunchCost = 5000.0;  // one extra launch, in tile_cost units (~3 us)
+
+bool tail_split_enabled() {
+    const char *s = getenv("GEMMKIT_HIP_TAILSPLIT");
+    return !(s && !strcmp(s, "0"));
+}
+
+bool plan_tail_split(int64_t M, int64_t N, int64_t kbytes, EpiKind kind, InType in, Tile t,
+                     double cost_whole, TailSplit *out) {
+    const TileCand &c = tile_cand(t);
+    const int64_t cus = g_num_cus > 0 ? g_num_cus : 256;
+    const int64_t tiles_m = (M + c.bm - 1) / c.bm, tiles_n = (N + c.bn - 1) / c.bn;
+    const int64_t rounds = (tiles_m * tiles_n + cus - 1) / cus;
+    if (rounds < 2) return false;
+    const int64_t tn_a = (rounds - 1) * cus / tiles_m;  // tile columns of the full rounds
+    if (tn_a <= 0 || tn_a >= tiles_n) return false;
+    const int64_t na = tn_a * c.bn;
+    const double cost_a = tile_cost(c, M, na, 1, kbytes, kind, in);
+    double best_b = 1e300;
+    Tile tb = Tile::T256x128;
+    for (Tile cand : {Tile::T256x128, Tile::T128x128}) {
+        const double cb = tile_cost(tile_cand(cand), M, N - na, 1, kbytes, kind, in);
+        if (cb < best_b) { best_b = cb; tb = cand; }
+    }
+    if (cost_a + best_b + kLaunchCost >= cost_whole) return false;
+    *out = TailSplit{na, t, tb};
+    return true;
 }
 
 // Split K: when the 64 x 64 tiles of one product leave most CUs idle and K is
@@ -561,7 +618,37 @@ int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t
         if (e != hipSuccess) return hip_fail(e, "split reduce launch");
         return finish("mfma gemm (split K)");
     }
-    e = launch_mma(in, pick_tile(M, N, batch, k * (int64_t)esz, ep.kind, in), args, ep, tl_stream);
+    const int64_t kbytes = k * (int64_t)esz;
+    double cost_whole = 0.0;
+    const Tile tile = pick_tile(M, N, batch, kbytes, ep.kind, in, &cost_whole);
+    bool forced;
+    env_tile(&forced);
+    TailSplit ts;
+    if (!forced && batch == 1 && tail_split_enabled() &&
+        plan_tail_split(M, N, kbytes, ep.kind, in, tile, cost_whole, &ts)) {
+        // Kernel-frame columns [0, na) with the chosen tile, [na, N) with a
+        // 128-wide one: B^T rows, C columns and, for per-column channels, the
+        // scales, biases and fused biases start na further on.
+        MmaArgs a1 = args, a2 = args;
+        a1.N = (int32_t)ts.na;
+        a2.N = (int32_t)(N - ts.na);
+        a2.b = (const uint8_t *)Bt.p + ts.na * Bt.rs * (int64_t)esz;
+        EpiParams e2 = ep;
+        const int64_t osz = ep.kind == EpiKind::Q8 ? 1 : (ep.kind == EpiKind::BF16 ? 2 : 4);
+        e2.c = (uint8_t *)ep.c + ts.na * ep.csc * osz;
+        if (ep.axis == 1) {
+            if (e2.scales) e2.scales += ts.na;
+            if (e2.bias) e2.bias += ts.na;
+            if (e2.fbias)
+                e2.fbias = (const uint8_t *)e2.fbias + ts.na * (ep.kind == EpiKind::BF16 ? 2 : 4);
+        }
+        e = launch_mma(in, ts.ta, a1, ep, tl_stream);
+        if (e != hipSuccess) return hip_fail(e, "mfma launch");
+        e = launch_mma(in, ts.tb, a2, e2, tl_stream);
+        if (e != hipSuccess) return hip_fail(e, "mfma launch");
+        return finish("mfma gemm (tail split)");
+    }
+    e = launch_mma(in, tile, args, ep, tl_stream);
     if (e != hipSuccess) return hip_fail(e, "mfma launch");
     return finish("mfma gemm");
 }
@@ -1059,6 +1146,29 @@ extern "C" {
 const char *gk_last_error(void) { return tl_error.c_str(); }
 
 const char *gk_version(void) { return "gemmkit-hip 0.1.0 (gfx950)"; }
+
+int gk_debug_plan(int32_t in, int32_t kind, int64_t m, int64_t n, int64_t batch, int64_t kbytes,
+                  int32_t *tile, int64_t *na, int32_t *tile_b) {
+    if (in < 0 || in > 2 || kind < 0 || kind > 3 || m <= 0 || n <= 0 || batch <= 0 ||
+        kbytes < 0 || !tile || !na || !tile_b)
+        return fail(GK_ERR_ARG, "gemmkit: gk_debug_plan: bad argument");
+    const InType it = (InType)in;
+    const EpiKind ek = (EpiKind)kind;
+    double cost_whole = 0.0;
+    const Tile t = pick_tile(m, n, batch, kbytes, ek, it, &cost_whole);
+    bool forced;
+    env_tile(&forced);
+    TailSplit ts;
+    *tile = (int32_t)t;
+    *na = 0;
+    *tile_b = (int32_t)t;
+    if (!forced && batch == 1 && tail_split_enabled() &&
+        plan_tail_split(m, n, kbytes, ek, it, t, cost_whole, &ts)) {
+        *na = ts.na;
+        *tile_b = (int32_t)ts.tb;
+    }
+    return ok();
+}
 
 int gk_init(void) {
     int r = device_init();

@@ -305,11 +305,19 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     // bytes at +16*l, i.e. stage row q*RPI + l/CPR, slot l%CPR, which holds
     // chunk (l%CPR) ^ swz(row).  Each instruction covers RPI whole rows, all
     // of A or all of B (BM is a multiple of RPI), so from_a is wave-uniform.
-    uint32_t voff[NIW];
-    int kch[NIW];
-    bool from_a[NIW];
+    // When all of a wave's rows come from one operand (WAVE_OP: every tile
+    // here but 256x128), instruction i's rows lie RPI*i rows below
+    // instruction 0's and its chunk differs only through the swizzle, which
+    // repeats every NPAT instructions; the offsets are then formed per load
+    // from NPAT bases (fewer live registers), else kept per instruction.
+    constexpr bool WAVE_OP = (BM % (NIW * RPI)) == 0;
+    constexpr int NPAT = BK == 128 ? 2 : 1;
+    constexpr int NOFF = WAVE_OP ? NPAT : NIW;
+    uint32_t voff[NOFF];
+    int kch[NOFF];
+    bool from_a[NOFF];
 #pragma unroll
-    for (int i = 0; i < NIW; ++i) {
+    for (int i = 0; i < NOFF; ++i) {
         const int q = wave * NIW + i;
         const int row = q * RPI + lane / CPR;
         const int ch = (lane % CPR) ^ swz_of<BK>(row);
@@ -318,6 +326,15 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
         voff[i] = from_a[i] ? (uint32_t)(row * lda_b + ch * 16)
                             : (uint32_t)((row - BM) * ldb_b + ch * 16);
     }
+    const uint32_t rstep = (uint32_t)(RPI * (from_a[0] ? lda_b : ldb_b));
+    auto lane_off = [&](int i) -> uint32_t {
+        if constexpr (WAVE_OP)
+            return voff[i % NPAT] + (uint32_t)(i - i % NPAT) * rstep;
+        else
+            return voff[i];
+    };
+    auto lane_kch = [&](int i) { return kch[WAVE_OP ? i % NPAT : i]; };
+    auto lane_from_a = [&](int i) { return from_a[WAVE_OP ? 0 : i]; };
     // Loads of stage kt into ring slot `slot`.  Stages past the end of K load
     // nothing but zeros (every lane out of range), as do the chunks past K of
     // a partial last stage.
@@ -328,9 +345,10 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
         const bool tail = !k_whole && kt == KT - 1;
 #pragma unroll
         for (int i = first; i < first + count; ++i) {
-            uint32_t off = voff[i] + kb;
-            if (dead || (tail && (int64_t)kb + kch[i] >= kbytes)) off = kOutOfRange;
-            dma16(from_a[i] ? a_pan : b_pan, from_a[i] ? a_num : b_num, off, dst + i * 1024);
+            uint32_t off = lane_off(i) + kb;
+            if (dead || (tail && (int64_t)kb + lane_kch(i) >= kbytes)) off = kOutOfRange;
+            dma16(lane_from_a(i) ? a_pan : b_pan, lane_from_a(i) ? a_num : b_num, off,
+                  dst + i * 1024);
         }
     };
     // Loads of a stage wholly inside K: the stage offset goes in the scalar
@@ -340,7 +358,6 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     // rows' bytes of a whole stage lie inside the resource.  When every wave's
     // rows come from one operand (the tiles here but 256x128), the wave keeps
     // one resource.
-    constexpr bool WAVE_OP = (BM % (NIW * RPI)) == 0;
     const bool w_from_a = wave * NIW * RPI < BM;
     const uint8_t *const w_pan = w_from_a ? a_pan : b_pan;
     const uint32_t w_num = w_from_a ? a_num : b_num;
@@ -351,7 +368,7 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
 #pragma unroll
         for (int i = first; i < first + count; ++i) {
             if constexpr (WAVE_OP)
-                dma16s(w_pan, w_num, voff[i], kb, dst + i * 1024);
+                dma16s(w_pan, w_num, lane_off(i), kb, dst + i * 1024);
             else
                 dma16s(from_a[i] ? a_pan : b_pan, from_a[i] ? a_num : b_num, voff[i], kb,
                        dst + i * 1024);

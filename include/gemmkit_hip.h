@@ -51,6 +51,17 @@ const char *gk_last_error(void);
 /* Library version string. */
 const char *gk_version(void);
 
+/* Launch plan of the matrix-core route for a product in the kernel frame (M x N
+ * output, K bytes per operand row; in: 0 int8, 1 bf16, 2 f32; kind: 0 i32,
+ * 1 f32, 2 bf16, 3 requantized i8/u8 output), as the dispatcher would choose
+ * it with the current environment: *tile is the tile of the (first) launch,
+ * *na the kernel-frame columns it covers when the product is split into two
+ * launches (else 0), *tile_b the tile of the second launch.  Host-only, no
+ * device needed.  No counterpart in the reference: it exposes the tile choice
+ * to tests and tuning tools. */
+int gk_debug_plan(int32_t in, int32_t kind, int64_t m, int64_t n, int64_t batch, int64_t kbytes,
+                  int32_t *tile, int64_t *na, int32_t *tile_b);
+
 /* ---------------------------------------------------------------- runtime */
 
 /* Parallelism request (src/parallel.rs:25): 1 = Serial, 0 = Rayon(0) "all",

@@ -1,0 +1,121 @@
+"""GPU parity of the tail split: products whose tiles take two rounds of the
+CUs with a short last round run as two launches (the full rounds' columns with
+the chosen tile, the rest with a 128-wide tile).  Every output element keeps
+its K order, so the results must equal the single launch
+(GEMMKIT_HIP_TAILSPLIT=0) bit for bit, for every epilogue: alpha/beta,
+requantization with per-column and per-row channels, fused bias and ReLU, and
+the orientation swap of a column-major C."""
+import os
+
+import pytest
+import torch
+
+import gemmkit_amd as gk
+
+pytestmark = pytest.mark.gpu
+
+
+class split_off:
+    def __enter__(self):
+        self.old = os.environ.get("GEMMKIT_HIP_TAILSPLIT")
+        os.environ["GEMMKIT_HIP_TAILSPLIT"] = "0"
+
+    def __exit__(self, *exc):
+        if self.old is None:
+            del os.environ["GEMMKIT_HIP_TAILSPLIT"]
+        else:
+            os.environ["GEMMKIT_HIP_TAILSPLIT"] = self.old
+
+
+def both(call):
+    """Runs call() with the split on, then off; returns the two outputs."""
+    on = call()
+    with split_off():
+        off = call()
+    return on, off
+
+
+def bits(t):
+    return t.view(torch.int8 if t.element_size() == 1 else
+                  torch.int16 if t.element_size() == 2 else torch.int32)
+
+
+def rand_i8(n, seed, dev, lo=-128):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(lo, 128, (n,), dtype=torch.int8, generator=g).to(dev)
+
+
+@pytest.mark.parametrize("c_col_major", [False, True])
+def test_i8_alpha_beta(dev, c_col_major):
+    m, k, n = 2048, 4096, 11008
+    if c_col_major:
+        m, n = n, m  # kernel frame: M = 2048, N = 11008 after the swap
+    assert gk.debug_plan("i8", "i32", 2048, 11008, k)[1] > 0
+    a, b = rand_i8(m * k, 1, dev), rand_i8(k * n, 2, dev)
+    g = torch.Generator().manual_seed(3)
+    c0 = torch.randint(-1000, 1000, (m * n,), dtype=torch.int32, generator=g).to(dev)
+    C = (lambda t: gk.MatMut.from_col_major(t, m, n)) if c_col_major else \
+        (lambda t: gk.MatMut.from_row_major(t, m, n))
+
+    def call():
+        c = c0.clone()
+        gk.gemm_i8(3, gk.MatRef.from_row_major(a, m, k), gk.MatRef(b, k, n, 1, k), -2, C(c))
+        return c
+    on, off = both(call)
+    assert torch.equal(on, off)
+
+
+@pytest.mark.parametrize("axis,u8", [(1, False), (0, True)])
+def test_requant(dev, axis, u8):
+    m, k, n = 2048, 4096, 11008
+    assert gk.debug_plan("i8", "q8", m, n, k)[1] > 0
+    a, b = rand_i8(m * k, 4, dev, -127), rand_i8(n * k, 5, dev, -127)
+    ch = n if axis else m
+    g = torch.Generator().manual_seed(6)
+    scales = (1e-4 + torch.rand(ch, generator=g) * (1e-2 - 1e-4)).to(dev)
+    bias = torch.randint(-65536, 65537, (ch,), dtype=torch.int32, generator=g).to(dev)
+    req = gk.Requantize(gk.RequantScale.PerCol(scales) if axis else gk.RequantScale.PerRow(scales),
+                        zero_point=7 if u8 else -3, bias=bias, bias_axis="col" if axis else "row",
+                        relu=True)
+    fn = gk.gemm_i8_requant_u8 if u8 else gk.gemm_i8_requant
+
+    def call():
+        c = torch.zeros(m * n, dtype=torch.uint8 if u8 else torch.int8, device=dev)
+        fn(gk.MatRef.from_row_major(a, m, k), gk.MatRef(b, k, n, 1, k), req,
+           gk.MatMut.from_row_major(c, m, n))
+        return c
+    on, off = both(call)
+    assert torch.equal(on, off)
+
+
+def test_bf16_fused_bias_relu(dev):
+    m, k, n = 2048, 2048, 8448
+    assert gk.debug_plan("bf16", "bf16", m, n, 2 * k)[1] > 0
+    g = torch.Generator().manual_seed(7)
+    a = torch.randn(m * k, generator=g).to(torch.bfloat16).to(dev)
+    b = torch.randn(k * n, generator=g).to(torch.bfloat16).to(dev)
+    bias = torch.randn(n, generator=g).to(torch.bfloat16).to(dev)
+
+    def call():
+        c = torch.zeros(m * n, dtype=torch.bfloat16, device=dev)
+        gk.gemm_fused(1.0, gk.MatRef.from_row_major(a, m, k), gk.MatRef(b, k, n, 1, k), 0.0,
+                      gk.MatMut.from_row_major(c, m, n), gk.Bias.PerCol(bias), gk.Activation.Relu)
+        return c
+    on, off = both(call)
+    assert torch.equal(bits(on), bits(off))
+
+
+def test_f32(dev):
+    m, k, n = 2048, 2048, 8448
+    assert gk.debug_plan("f32", "f32", m, n, 4 * k)[1] > 0
+    g = torch.Generator().manual_seed(8)
+    a = torch.rand(m * k, generator=g).to(dev) * 2 - 1
+    b = torch.rand(k * n, generator=g).to(dev) * 2 - 1
+
+    def call():
+        c = torch.zeros(m * n, dtype=torch.float32, device=dev)
+        gk.gemm(1.0, gk.MatRef.from_row_major(a, m, k), gk.MatRef.from_row_major(b, k, n), 0.0,
+                gk.MatMut.from_row_major(c, m, n))
+        return c
+    on, off = both(call)
+    assert torch.equal(bits(on), bits(off))

@@ -1,0 +1,71 @@
+"""Host-side launch plan (no device needed): the tile choice of the fitted
+cost model and the two-launch tail split, through gk_debug_plan.
+
+The expected tiles are the measured best forced tiles of the 13-shape sweep the
+model was fitted to (gemmkit_amd/calibrate_tiles.py), so a refit that loses one
+of them fails here."""
+import os
+
+import pytest
+
+import gemmkit_amd as gk
+
+# (in, output kind, M, N, K bytes, batch) -> measured best tile
+SWEEP = [
+    (("i8", "i32", 4096, 4096, 4096, 1), "256x256k128"),
+    (("i8", "q8", 2048, 11008, 4096, 1), "256x256w8k128"),
+    (("i8", "i32", 2048, 11008, 4096, 1), "256x256w8k128"),
+    (("i8", "i32", 8192, 8192, 1024, 1), "128x128"),
+    (("i8", "i32", 1024, 1024, 8192, 1), "64x64"),
+    (("i8", "i32", 3000, 5000, 2000, 1), "256x256k128"),
+    (("i8", "q8", 4096, 4096, 4096, 1), "256x256w8k128"),
+    (("bf16", "f32", 4096, 4096, 8192, 1), "256x256w8k128"),
+    (("bf16", "f32", 512, 512, 256, 64), "256x256w8k128"),
+    (("bf16", "bf16", 2048, 11008, 8192, 1), "256x256w8k128"),
+    (("bf16", "bf16", 2048, 2048, 4096, 1), "128x128"),
+    (("f32", "f32", 2048, 2048, 8192, 1), "128x128"),
+    (("f32", "f32", 1024, 1024, 4096, 1), "64x64"),
+]
+
+
+@pytest.fixture
+def clean_env(monkeypatch):
+    monkeypatch.delenv("GEMMKIT_HIP_TILE", raising=False)
+    monkeypatch.delenv("GEMMKIT_HIP_TAILSPLIT", raising=False)
+
+
+@pytest.mark.parametrize("shape,best", SWEEP)
+def test_model_picks_the_measured_best_tile(clean_env, shape, best):
+    assert gk.debug_plan(*shape)[0] == best
+
+
+@pytest.mark.parametrize("shape,tile_b", [
+    (("i8", "q8", 2048, 11008, 4096), "128x128"),
+    (("i8", "i32", 2048, 11008, 4096), "256x128"),
+    (("bf16", "bf16", 2048, 11008, 8192), "256x128"),
+])
+def test_tail_split_of_the_layer_shapes(clean_env, shape, tile_b):
+    # 8 x 43 tiles of 256: the first 32 tile columns fill one round of 256 CUs
+    tile, na, tb = gk.debug_plan(*shape)
+    assert (tile, na, tb) == ("256x256w8k128", 8192, tile_b)
+
+
+def test_no_split_for_one_round(clean_env):
+    assert gk.debug_plan("i8", "i32", 4096, 4096, 4096)[1] == 0
+    assert gk.debug_plan("bf16", "f32", 4096, 4096, 8192)[1] == 0
+
+
+def test_split_switches(clean_env, monkeypatch):
+    monkeypatch.setenv("GEMMKIT_HIP_TAILSPLIT", "0")
+    assert gk.debug_plan("i8", "q8", 2048, 11008, 4096)[1] == 0
+    monkeypatch.delenv("GEMMKIT_HIP_TAILSPLIT")
+    monkeypatch.setenv("GEMMKIT_HIP_TILE", "256x256")
+    assert gk.debug_plan("i8", "q8", 2048, 11008, 4096) == ("256x256", 0, "256x256")
+    # batched products never split (the split is per element shape only)
+    monkeypatch.delenv("GEMMKIT_HIP_TILE")
+    assert gk.debug_plan("i8", "q8", 2048, 11008, 4096, 2)[1] == 0
+
+
+def test_bad_arguments():
+    with pytest.raises(gk.GemmkitError):
+        gk.debug_plan("i8", "i32", 0, 16, 16)
