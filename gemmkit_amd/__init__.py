@@ -501,6 +501,88 @@ def gemm_batched(batch: int, alpha, a: MatRef, a_batch_stride: int, b: MatRef,
         raise TypeError(f"gemmkit_amd: gemm_batched supports float32 and bfloat16, got {dt}")
 
 
+@dataclass
+class GemmProblem:
+    """GemmProblem (src/dispatch.rs:135-164): one independent product of the
+    pointer-array batched form; a, b, c are device tensors (element offsets
+    a_off, b_off, c_off), all float32 or all bfloat16."""
+    m: int
+    k: int
+    n: int
+    alpha: float
+    a: torch.Tensor
+    rsa: int
+    csa: int
+    b: torch.Tensor
+    rsb: int
+    csb: int
+    beta: float
+    c: torch.Tensor
+    rsc: int
+    csc: int
+    a_off: int = 0
+    b_off: int = 0
+    c_off: int = 0
+
+
+@dataclass
+class BatchProblem:
+    """BatchProblem (src/api/batched.rs:723-735): one element of gemm_batched_slice."""
+    alpha: float
+    a: MatRef
+    b: MatRef
+    beta: float
+    c: MatMut
+
+
+def gemm_batched_ptr_unchecked(problems, par: Optional[Parallelism] = None,
+                               ws: Optional[Workspace] = None) -> None:
+    """``gemm_batched_ptr_unchecked`` (src/api/batched.rs:711-720): every problem as the
+    standalone gemm would run it; the outputs must be pairwise disjoint."""
+    _bind_stream()
+    if not problems:
+        return
+    L = _lib.lib()
+    dt = problems[0].a.dtype
+    if dt == torch.float32:
+        arr = (_lib.ProblemF32C * len(problems))(*[
+            _lib.ProblemF32C(p.m, p.k, p.n, float(p.alpha), _ptr(p.a, p.a_off), p.rsa, p.csa,
+                             _ptr(p.b, p.b_off), p.rsb, p.csb, float(p.beta), _ptr(p.c, p.c_off),
+                             p.rsc, p.csc) for p in problems])
+        _check(L.gk_gemm_batched_ptr_f32_unchecked(_ws(ws), arr, len(problems), _par(par)))
+    elif dt == torch.bfloat16:
+        arr = (_lib.ProblemBf16C * len(problems))(*[
+            _lib.ProblemBf16C(p.m, p.k, p.n, _bf16_bits(p.alpha), _ptr(p.a, p.a_off), p.rsa,
+                              p.csa, _ptr(p.b, p.b_off), p.rsb, p.csb, _bf16_bits(p.beta),
+                              _ptr(p.c, p.c_off), p.rsc, p.csc) for p in problems])
+        _check(L.gk_gemm_batched_ptr_bf16_unchecked(_ws(ws), arr, len(problems), _par(par)))
+    else:
+        raise TypeError("gemmkit_amd: gemm_batched_ptr_unchecked supports float32 and bfloat16")
+
+
+def gemm_batched_slice(problems, par: Optional[Parallelism] = None,
+                       ws: Optional[Workspace] = None) -> None:
+    """``gemm_batched_slice`` (src/api/batched.rs:748-799): per-element shape, bounds and
+    self-alias checks, then the pointer-array run."""
+    _bind_stream()
+    if not problems:
+        return
+    L = _lib.lib()
+    dt = problems[0].a.data.dtype
+    if dt == torch.float32:
+        arr = (_lib.BatchProblemF32C * len(problems))(*[
+            _lib.BatchProblemF32C(float(p.alpha), p.a._c(dt, "A"), p.b._c(dt, "B"),
+                                  float(p.beta), p.c._c(dt, "C")) for p in problems])
+        _check(L.gk_gemm_batched_slice_f32(_ws(ws), arr, len(problems), _par(par)))
+    elif dt == torch.bfloat16:
+        arr = (_lib.BatchProblemBf16C * len(problems))(*[
+            _lib.BatchProblemBf16C(_bf16_bits(p.alpha), p.a._c(dt, "A"), p.b._c(dt, "B"),
+                                   _bf16_bits(p.beta), p.c._c(dt, "C")) for p in problems])
+        _check(L.gk_gemm_batched_slice_bf16(_ws(ws), arr, len(problems), _par(par)))
+    else:
+        raise TypeError("gemmkit_amd: gemm_batched_slice supports float32 and bfloat16")
+
+
 def gemm_batched_unchecked(batch, m, k, n, alpha, a, rsa, csa, a_bs, b, rsb, csb, b_bs, beta,
                            c, rsc, csc, c_bs, par=None, ws=None) -> None:
     """``gemm_batched_unchecked(_with)`` (src/api/batched.rs:594-700)."""

@@ -46,6 +46,32 @@ class BiasC(C.Structure):
     _fields_ = [("data", _vp), ("len", _size), ("dim", _i32)]
 
 
+class ProblemF32C(C.Structure):
+    """``gk_problem_f32``: GemmProblem<f32> (src/dispatch.rs:135-164)."""
+    _fields_ = [("m", _size), ("k", _size), ("n", _size), ("alpha", _f32), ("a", _vp),
+                ("rsa", _sdiff), ("csa", _sdiff), ("b", _vp), ("rsb", _sdiff), ("csb", _sdiff),
+                ("beta", _f32), ("c", _vp), ("rsc", _sdiff), ("csc", _sdiff)]
+
+
+class ProblemBf16C(C.Structure):
+    """``gk_problem_bf16``: GemmProblem<bf16> (src/dispatch.rs:135-164)."""
+    _fields_ = [("m", _size), ("k", _size), ("n", _size), ("alpha", _u16), ("a", _vp),
+                ("rsa", _sdiff), ("csa", _sdiff), ("b", _vp), ("rsb", _sdiff), ("csb", _sdiff),
+                ("beta", _u16), ("c", _vp), ("rsc", _sdiff), ("csc", _sdiff)]
+
+
+class BatchProblemF32C(C.Structure):
+    """``gk_batch_problem_f32``: BatchProblem<f32> (src/api/batched.rs:723-735)."""
+    _fields_ = [("alpha", _f32), ("a", MatRefC), ("b", MatRefC), ("beta", _f32),
+                ("c", MatMutC)]
+
+
+class BatchProblemBf16C(C.Structure):
+    """``gk_batch_problem_bf16``: BatchProblem<bf16> (src/api/batched.rs:723-735)."""
+    _fields_ = [("alpha", _u16), ("a", MatRefC), ("b", MatRefC), ("beta", _u16),
+                ("c", MatMutC)]
+
+
 _REF = C.POINTER(MatRefC)
 _MUT = C.POINTER(MatMutC)
 _REQ = C.POINTER(RequantizeC)
@@ -118,6 +144,10 @@ SIGNATURES: dict[str, tuple] = {
                                                         _vp, _sdiff, _sdiff, _sdiff, _vp, _sdiff,
                                                         _sdiff, _sdiff, _f32, _vp, _sdiff, _sdiff,
                                                         _sdiff, _u32]),
+    "gk_gemm_batched_ptr_f32_unchecked": (C.c_int, [_vp, C.POINTER(ProblemF32C), _size, _u32]),
+    "gk_gemm_batched_ptr_bf16_unchecked": (C.c_int, [_vp, C.POINTER(ProblemBf16C), _size, _u32]),
+    "gk_gemm_batched_slice_f32": (C.c_int, [_vp, C.POINTER(BatchProblemF32C), _size, _u32]),
+    "gk_gemm_batched_slice_bf16": (C.c_int, [_vp, C.POINTER(BatchProblemBf16C), _size, _u32]),
     "gk_prepack_rhs_f32": (C.c_int, [_REF, C.POINTER(_vp)]),
     "gk_prepack_rhs_f32_unchecked": (C.c_int, [_vp, _sdiff, _sdiff, _size, _size,
                                                C.POINTER(_vp)]),

@@ -1137,6 +1137,101 @@ int packed_b_checked(gk_workspace *ws, InType in, EpiKind kind, size_t esz, floa
                               c->data, c->rs, c->cs, any ? &fx : nullptr);
 }
 
+// ---- pointer-array batched (src/api/batched.rs:711-799; run_ptr,
+// src/special/batched.rs:294-334: every problem as a standalone gemm)
+
+// Element step of a run of problems: the pointer difference in elements, when
+// it is a whole number of elements.
+bool elem_step(const void *p0, const void *p1, size_t esz, ptrdiff_t *step) {
+    const ptrdiff_t d = (const char *)p1 - (const char *)p0;
+    if (d % (ptrdiff_t)esz) return false;
+    *step = d / (ptrdiff_t)esz;
+    return true;
+}
+
+// Runs problems[0..count) of one element type: runs of consecutive problems
+// that share shape, scalars and strides with constant pointer steps go out as
+// one strided batched launch (each element bit-identical to the standalone
+// product, as gemm_batched's are), the others one by one.
+template <typename P, typename S>
+int run_problems(gk_workspace *ws, InType in, const P *problems, size_t count, S to_f32) {
+    const size_t esz = in_size(in);
+    const EpiKind kind = in == InType::F32 ? EpiKind::F32 : EpiKind::BF16;
+    size_t i = 0;
+    while (i < count) {
+        const P &p = problems[i];
+        size_t j = i + 1;
+        ptrdiff_t sa = 0, sb = 0, sc = 0;
+        // (a zero output step would be overlapping outputs, which the caller
+        // excludes; such problems run one by one, in order)
+        if (j < count && elem_step(p.a, problems[j].a, esz, &sa) &&
+            elem_step(p.b, problems[j].b, esz, &sb) && elem_step(p.c, problems[j].c, esz, &sc) &&
+            sc != 0) {
+            auto same = [&](const P &q, size_t idx) {
+                ptrdiff_t qa, qb, qc;
+                return q.m == p.m && q.k == p.k && q.n == p.n && q.rsa == p.rsa &&
+                       q.csa == p.csa && q.rsb == p.rsb && q.csb == p.csb && q.rsc == p.rsc &&
+                       q.csc == p.csc && !memcmp(&q.alpha, &p.alpha, sizeof p.alpha) &&
+                       !memcmp(&q.beta, &p.beta, sizeof p.beta) &&
+                       elem_step(p.a, q.a, esz, &qa) && qa == sa * (ptrdiff_t)(idx - i) &&
+                       elem_step(p.b, q.b, esz, &qb) && qb == sb * (ptrdiff_t)(idx - i) &&
+                       elem_step(p.c, q.c, esz, &qc) && qc == sc * (ptrdiff_t)(idx - i);
+            };
+            while (j < count && j - i < 65535 && same(problems[j], j)) ++j;
+        }
+        int r;
+        if (j - i > 1)
+            r = exec_float(ws, in, kind, j - i, p.m, p.k, p.n, to_f32(p.alpha), p.a, p.rsa, p.csa,
+                           sa, p.b, p.rsb, p.csb, sb, to_f32(p.beta), p.c, p.rsc, p.csc, sc);
+        else
+            r = exec_float(ws, in, kind, 1, p.m, p.k, p.n, to_f32(p.alpha), p.a, p.rsa, p.csa, 0,
+                           p.b, p.rsb, p.csb, 0, to_f32(p.beta), p.c, p.rsc, p.csc, 0);
+        if (r) return r;
+        i = j;
+    }
+    return ok();
+}
+
+// gemm_batched_slice's per-element checks (src/api/batched.rs:751-783).
+int validate_batch_problem(size_t i, const gk_mat_ref &a, const gk_mat_ref &b,
+                           const gk_mat_mut &c) {
+    if (a.cols != b.rows)
+        return fail(GK_ERR_SHAPE, "gemmkit: batch element %zu A.cols (%zu) != B.rows (%zu)", i,
+                    a.cols, b.rows);
+    if (a.rows != c.rows)
+        return fail(GK_ERR_SHAPE, "gemmkit: batch element %zu A.rows (%zu) != C.rows (%zu)", i,
+                    a.rows, c.rows);
+    if (b.cols != c.cols)
+        return fail(GK_ERR_SHAPE, "gemmkit: batch element %zu B.cols (%zu) != C.cols (%zu)", i,
+                    b.cols, c.cols);
+    int r;
+    if ((r = check_view(a.len, a.rows, a.cols, a.rs, a.cs, "A"))) return r;
+    if ((r = check_view(b.len, b.rows, b.cols, b.rs, b.cs, "B"))) return r;
+    if ((r = check_view(c.len, c.rows, c.cols, c.rs, c.cs, "C"))) return r;
+    if (self_aliases(c.rows, c.cols, c.rs, c.cs))
+        return fail(GK_ERR_ALIAS,
+                    "gemmkit: batch element %zu C view aliases itself (strides %td,%td); C must "
+                    "address each (i,j) uniquely",
+                    i, c.rs, c.cs);
+    return GK_OK;
+}
+
+template <typename BP, typename P, typename S>
+int batched_slice(gk_workspace *ws, const BP *problems, size_t count, gk_par par,
+                  int (*run)(gk_workspace *, const P *, size_t, gk_par)) {
+    if (count == 0) return ok();
+    if (!problems) return fail(GK_ERR_ARG, "gemmkit: null problems array");
+    std::vector<P> raw(count);
+    for (size_t i = 0; i < count; ++i) {
+        const BP &q = problems[i];
+        int r = validate_batch_problem(i, q.a, q.b, q.c);
+        if (r) return r;
+        raw[i] = P{q.a.rows, q.a.cols, q.b.cols, q.alpha, (const S *)q.a.data, q.a.rs, q.a.cs,
+                   (const S *)q.b.data, q.b.rs, q.b.cs, q.beta, (S *)q.c.data, q.c.rs, q.c.cs};
+    }
+    return run(ws, raw.data(), count, par);
+}
+
 }  // namespace
 
 // =============================================================== C ABI
@@ -1460,6 +1555,33 @@ int gk_gemm_batched_bf16(gk_workspace *ws, size_t batch, gk_bf16 alpha, const gk
                                           (const gk_bf16 *)a->data, a->rs, a->cs, a_bs,
                                           (const gk_bf16 *)b->data, b->rs, b->cs, b_bs, beta,
                                           (gk_bf16 *)c->data, c->rs, c->cs, c_bs, par);
+}
+
+int gk_gemm_batched_ptr_f32_unchecked(gk_workspace *ws, const gk_problem_f32 *problems,
+                                      size_t count, gk_par) {
+    if (count == 0) return ok();
+    if (!problems) return fail(GK_ERR_ARG, "gemmkit: null problems array");
+    return run_problems(ws, InType::F32, problems, count, [](float v) { return v; });
+}
+
+int gk_gemm_batched_ptr_bf16_unchecked(gk_workspace *ws, const gk_problem_bf16 *problems,
+                                       size_t count, gk_par) {
+    if (count == 0) return ok();
+    if (!problems) return fail(GK_ERR_ARG, "gemmkit: null problems array");
+    return run_problems(ws, InType::BF16, problems, count,
+                        [](gk_bf16 v) { return bf16_to_f32(v); });
+}
+
+int gk_gemm_batched_slice_f32(gk_workspace *ws, const gk_batch_problem_f32 *problems,
+                              size_t count, gk_par par) {
+    return batched_slice<gk_batch_problem_f32, gk_problem_f32, float>(
+        ws, problems, count, par, gk_gemm_batched_ptr_f32_unchecked);
+}
+
+int gk_gemm_batched_slice_bf16(gk_workspace *ws, const gk_batch_problem_bf16 *problems,
+                               size_t count, gk_par par) {
+    return batched_slice<gk_batch_problem_bf16, gk_problem_bf16, gk_bf16>(
+        ws, problems, count, par, gk_gemm_batched_ptr_bf16_unchecked);
 }
 
 int gk_gemm_batched_bf16_f32out_unchecked(gk_workspace *ws, size_t batch, size_t m, size_t k,

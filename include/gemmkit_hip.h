@@ -352,6 +352,72 @@ int gk_gemm_batched_bf16_f32out_unchecked(gk_workspace *ws, size_t batch, size_t
                                           ptrdiff_t rsc, ptrdiff_t csc, ptrdiff_t c_bs,
                                           gk_par par);
 
+/* ------------------------------------------ pointer-array batched GEMM */
+
+/* GemmProblem (src/dispatch.rs:135-164): one independent product with its own
+ * shape, scalars, device pointers and strides. */
+typedef struct gk_problem_f32 {
+    size_t m, k, n;
+    float alpha;
+    const float *a;
+    ptrdiff_t rsa, csa;
+    const float *b;
+    ptrdiff_t rsb, csb;
+    float beta;
+    float *c;
+    ptrdiff_t rsc, csc;
+} gk_problem_f32;
+
+typedef struct gk_problem_bf16 {
+    size_t m, k, n;
+    gk_bf16 alpha;
+    const gk_bf16 *a;
+    ptrdiff_t rsa, csa;
+    const gk_bf16 *b;
+    ptrdiff_t rsb, csb;
+    gk_bf16 beta;
+    gk_bf16 *c;
+    ptrdiff_t rsc, csc;
+} gk_problem_bf16;
+
+/* gemm_batched_ptr_unchecked (src/api/batched.rs:711-720): every problem of
+ * the host array runs as the standalone gemm would (bit for bit).  Runs of
+ * consecutive problems with one shape, one set of scalars and strides and
+ * constant pointer steps go out as one strided batched launch.  The caller
+ * guarantees what the reference's Safety section asks: valid pointers,
+ * outputs pairwise disjoint and aliasing no input. */
+int gk_gemm_batched_ptr_f32_unchecked(gk_workspace *ws, const gk_problem_f32 *problems,
+                                      size_t count, gk_par par);
+int gk_gemm_batched_ptr_bf16_unchecked(gk_workspace *ws, const gk_problem_bf16 *problems,
+                                       size_t count, gk_par par);
+
+/* BatchProblem (src/api/batched.rs:723-735): one element of the checked form. */
+typedef struct gk_batch_problem_f32 {
+    float alpha;
+    gk_mat_ref a;
+    gk_mat_ref b;
+    float beta;
+    gk_mat_mut c;
+} gk_batch_problem_f32;
+
+typedef struct gk_batch_problem_bf16 {
+    gk_bf16 alpha;
+    gk_mat_ref a;
+    gk_mat_ref b;
+    gk_bf16 beta;
+    gk_mat_mut c;
+} gk_batch_problem_bf16;
+
+/* gemm_batched_slice (src/api/batched.rs:748-799): per element, the shape
+ * agreement, view bounds and C self-alias checks with the reference's
+ * messages ("gemmkit: batch element i ..."), then the pointer-array run.  In
+ * the reference distinct &mut borrows make the outputs disjoint; here that is
+ * the caller's guarantee, as for the raw form. */
+int gk_gemm_batched_slice_f32(gk_workspace *ws, const gk_batch_problem_f32 *problems,
+                              size_t count, gk_par par);
+int gk_gemm_batched_slice_bf16(gk_workspace *ws, const gk_batch_problem_bf16 *problems,
+                               size_t count, gk_par par);
+
 /* --------------------------------------------- fused bias and activation */
 
 /* Bias (src/api/fused.rs:17-23) / BiasDim (src/kernel/epilogue.rs:205-210):

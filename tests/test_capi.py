@@ -239,3 +239,38 @@ def test_packed_fused_null_handle():
     assert rc == -4 and _lib.last_error() == "gemmkit: null argument"
     rc = L.gk_gemm_packed_b_f32_unchecked(None, 1.0, 4, FAKE_A, 4, 1, None, 0.0, FAKE_C, 1, 4, 1)
     assert rc == -4 and _lib.last_error() == "gemmkit: null packed RHS"
+
+
+def batch_problem(a, b, c, alpha=1.0, beta=0.0):
+    return _lib.BatchProblemF32C(alpha, a, b, beta, c)
+
+
+@pytest.mark.parametrize("bad,msg", [
+    ((ref(FAKE_A, 100, 10, 9, 9, 1), ref(FAKE_B, 100, 10, 10, 10, 1), mut(FAKE_C, 100, 10, 10, 10, 1)),
+     "gemmkit: batch element 1 A.cols (9) != B.rows (10)"),
+    ((ref(FAKE_A, 100, 10, 10, 10, 1), ref(FAKE_B, 100, 10, 10, 10, 1), mut(FAKE_C, 100, 9, 10, 10, 1)),
+     "gemmkit: batch element 1 A.rows (10) != C.rows (9)"),
+    ((ref(FAKE_A, 100, 10, 10, 10, 1), ref(FAKE_B, 100, 10, 9, 9, 1), mut(FAKE_C, 100, 10, 10, 10, 1)),
+     "gemmkit: batch element 1 B.cols (9) != C.cols (10)"),
+    ((ref(FAKE_A, 99, 10, 10, 10, 1), ref(FAKE_B, 100, 10, 10, 10, 1), mut(FAKE_C, 100, 10, 10, 10, 1)),
+     "gemmkit: A view of 10x10 (strides 10,1) needs 100 elements but slice has 99"),
+    ((ref(FAKE_A, 100, 10, 10, -10, 1), ref(FAKE_B, 100, 10, 10, 10, 1), mut(FAKE_C, 100, 10, 10, 10, 1)),
+     "gemmkit: A view has negative strides or is too large to address; use gemm_unchecked"),
+    ((ref(FAKE_A, 100, 10, 10, 10, 1), ref(FAKE_B, 100, 10, 10, 10, 1), mut(FAKE_C, 100, 10, 10, 5, 1)),
+     "gemmkit: batch element 1 C view aliases itself (strides 5,1); C must address each (i,j) "
+     "uniquely"),
+])
+def test_batched_slice_validation(bad, msg):
+    # element 0 is valid; element 1 fails with gemm_batched_slice's message
+    # (src/api/batched.rs:751-783), before any device work
+    ok = batch_problem(ref(FAKE_A, 100, 10, 10, 10, 1), ref(FAKE_B, 100, 10, 10, 10, 1),
+                       mut(FAKE_C + 4096, 100, 10, 10, 10, 1))
+    arr = (_lib.BatchProblemF32C * 2)(ok, batch_problem(*bad))
+    rc = _lib.lib().gk_gemm_batched_slice_f32(None, arr, 2, 1)
+    assert rc < 0
+    assert _lib.last_error() == msg
+
+
+def test_batched_ptr_empty_is_a_no_op():
+    assert _lib.lib().gk_gemm_batched_ptr_f32_unchecked(None, None, 0, 1) == 0
+    assert _lib.lib().gk_gemm_batched_slice_bf16(None, None, 0, 1) == 0
