@@ -841,3 +841,125 @@ def gemm_packed_b_fused_unchecked(alpha, m, a, rsa, csa, packed: PackedRhs, beta
             _bf16_bits(beta), _ptr(c, c_off), rsc, csc, bp, bd, hb, kind, slope, _par(par)))
     else:
         raise TypeError("gemmkit_amd: gemm_packed_b_fused_unchecked supports float32 and bfloat16")
+
+
+# ------------------------------------------------------------ prepacked LHS
+
+class PackedLhs:
+    """PackedLhs<T> (src/api/packed.rs:953-981): A packed once on the device,
+    float32 or bfloat16 (:func:`prepack_lhs`)."""
+
+    def __init__(self, handle, dtype: torch.dtype):
+        self._free = _lib.lib().gk_packed_lhs_free  # held so __del__ works during interpreter exit
+        self._h = handle
+        self.dtype = dtype
+
+    @property
+    def handle(self):
+        return self._h
+
+    def rows(self) -> int:
+        return int(_lib.lib().gk_packed_lhs_rows(self._h))
+
+    def cols(self) -> int:
+        return int(_lib.lib().gk_packed_lhs_cols(self._h))
+
+    def __del__(self) -> None:
+        h, self._h = getattr(self, "_h", None), None
+        if h:
+            self._free(h)
+
+
+def prepack_lhs(a: MatRef) -> PackedLhs:
+    """``prepack_lhs::<f32|bf16>`` (src/api/packed.rs:986-996)."""
+    _bind_stream()
+    L = _lib.lib()
+    out = C.c_void_p()
+    dt = a.data.dtype
+    if dt == torch.float32:
+        _check(L.gk_prepack_lhs_f32(a._c(dt, "A"), C.byref(out)))
+    elif dt == torch.bfloat16:
+        _check(L.gk_prepack_lhs_bf16(a._c(dt, "A"), C.byref(out)))
+    else:
+        raise TypeError(f"gemmkit_amd: prepack_lhs supports float32 and bfloat16, got {dt}")
+    return PackedLhs(out.value, dt)
+
+
+def prepack_lhs_unchecked(a: torch.Tensor, rsa, csa, m, k, a_off=0) -> PackedLhs:
+    """``prepack_lhs_unchecked`` (src/api/packed.rs:999-1030)."""
+    _bind_stream()
+    L = _lib.lib()
+    out = C.c_void_p()
+    fn = L.gk_prepack_lhs_f32_unchecked if a.dtype == torch.float32 else \
+        L.gk_prepack_lhs_bf16_unchecked
+    _check(fn(_ptr(a, a_off), rsa, csa, m, k, C.byref(out)))
+    return PackedLhs(out.value, a.dtype)
+
+
+def gemm_packed_a(alpha, packed: PackedLhs, b: MatRef, beta, c: MatMut,
+                  par: Optional[Parallelism] = None, ws: Optional[Workspace] = None) -> None:
+    """``gemm_packed_a(_with)`` (src/api/packed.rs:1049-1140): row-major-ish C."""
+    _bind_stream()
+    L = _lib.lib()
+    dt = b.data.dtype
+    if dt == torch.float32:
+        _check(L.gk_gemm_packed_a_f32(_ws(ws), float(alpha), packed.handle, b._c(dt, "B"),
+                                      float(beta), c._c(dt, "C"), _par(par)))
+    elif dt == torch.bfloat16:
+        _check(L.gk_gemm_packed_a_bf16(_ws(ws), _bf16_bits(alpha), packed.handle, b._c(dt, "B"),
+                                       _bf16_bits(beta), c._c(dt, "C"), _par(par)))
+    else:
+        raise TypeError(f"gemmkit_amd: gemm_packed_a supports float32 and bfloat16, got {dt}")
+
+
+def gemm_packed_a_unchecked(alpha, packed: PackedLhs, n, b, rsb, csb, beta, c, rsc, csc,
+                            par=None, ws=None, b_off=0, c_off=0) -> None:
+    """``gemm_packed_a_unchecked(_with)`` (src/api/packed.rs:1143-1240)."""
+    _bind_stream()
+    L = _lib.lib()
+    if b.dtype == torch.float32:
+        _check(L.gk_gemm_packed_a_f32_unchecked(_ws(ws), float(alpha), packed.handle, n,
+                                                _ptr(b, b_off), rsb, csb, float(beta),
+                                                _ptr(c, c_off), rsc, csc, _par(par)))
+    else:
+        _check(L.gk_gemm_packed_a_bf16_unchecked(_ws(ws), _bf16_bits(alpha), packed.handle, n,
+                                                 _ptr(b, b_off), rsb, csb, _bf16_bits(beta),
+                                                 _ptr(c, c_off), rsc, csc, _par(par)))
+
+
+def gemm_packed_a_fused(alpha, packed: PackedLhs, b: MatRef, beta, c: MatMut,
+                        bias: Optional[Bias] = None, act: Optional[Activation] = None,
+                        par: Optional[Parallelism] = None, ws: Optional[Workspace] = None) -> None:
+    """``gemm_packed_a_fused(_with)`` (src/api/packed.rs:1250-1365)."""
+    _bind_stream()
+    L = _lib.lib()
+    dt = b.data.dtype
+    bc, kind, slope = _fused_args(dt, bias, act)
+    if dt == torch.float32:
+        _check(L.gk_gemm_packed_a_fused_f32(_ws(ws), float(alpha), packed.handle, b._c(dt, "B"),
+                                            float(beta), c._c(dt, "C"), bc, kind, slope,
+                                            _par(par)))
+    elif dt == torch.bfloat16:
+        _check(L.gk_gemm_packed_a_fused_bf16(_ws(ws), _bf16_bits(alpha), packed.handle,
+                                             b._c(dt, "B"), _bf16_bits(beta), c._c(dt, "C"), bc,
+                                             kind, slope, _par(par)))
+    else:
+        raise TypeError(f"gemmkit_amd: gemm_packed_a_fused supports float32 and bfloat16, got {dt}")
+
+
+def gemm_packed_a_fused_unchecked(alpha, packed: PackedLhs, n, b, rsb, csb, beta, c, rsc, csc,
+                                  bias=None, bias_dim=0, act=0, slope=0.0, par=None, ws=None,
+                                  b_off=0, c_off=0) -> None:
+    """``gemm_packed_a_fused_unchecked(_with)`` (src/api/packed.rs:1369-1440)."""
+    _bind_stream()
+    L = _lib.lib()
+    bp, bd, hb = _raw_bias(bias, bias_dim)
+    if b.dtype == torch.float32:
+        _check(L.gk_gemm_packed_a_fused_f32_unchecked(
+            _ws(ws), float(alpha), packed.handle, n, _ptr(b, b_off), rsb, csb, float(beta),
+            _ptr(c, c_off), rsc, csc, bp, bd, hb, int(act), float(slope), _par(par)))
+    else:
+        _check(L.gk_gemm_packed_a_fused_bf16_unchecked(
+            _ws(ws), _bf16_bits(alpha), packed.handle, n, _ptr(b, b_off), rsb, csb,
+            _bf16_bits(beta), _ptr(c, c_off), rsc, csc, bp, bd, hb, int(act), _bf16_bits(slope),
+            _par(par)))

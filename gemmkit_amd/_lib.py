@@ -154,6 +154,31 @@ SIGNATURES: dict[str, tuple] = {
     "gk_prepack_rhs_bf16": (C.c_int, [_REF, C.POINTER(_vp)]),
     "gk_prepack_rhs_bf16_unchecked": (C.c_int, [_vp, _sdiff, _sdiff, _size, _size,
                                                 C.POINTER(_vp)]),
+    "gk_prepack_lhs_f32": (C.c_int, [_REF, C.POINTER(_vp)]),
+    "gk_prepack_lhs_f32_unchecked": (C.c_int, [_vp, _sdiff, _sdiff, _size, _size,
+                                               C.POINTER(_vp)]),
+    "gk_prepack_lhs_bf16": (C.c_int, [_REF, C.POINTER(_vp)]),
+    "gk_prepack_lhs_bf16_unchecked": (C.c_int, [_vp, _sdiff, _sdiff, _size, _size,
+                                                C.POINTER(_vp)]),
+    "gk_packed_lhs_free": (None, [_vp]),
+    "gk_packed_lhs_rows": (_size, [_vp]),
+    "gk_packed_lhs_cols": (_size, [_vp]),
+    "gk_gemm_packed_a_f32": (C.c_int, [_vp, _f32, _vp, _REF, _f32, _MUT, _u32]),
+    "gk_gemm_packed_a_bf16": (C.c_int, [_vp, _u16, _vp, _REF, _u16, _MUT, _u32]),
+    "gk_gemm_packed_a_f32_unchecked": (C.c_int, [_vp, _f32, _vp, _size, _vp, _sdiff, _sdiff,
+                                                 _f32, _vp, _sdiff, _sdiff, _u32]),
+    "gk_gemm_packed_a_bf16_unchecked": (C.c_int, [_vp, _u16, _vp, _size, _vp, _sdiff, _sdiff,
+                                                  _u16, _vp, _sdiff, _sdiff, _u32]),
+    "gk_gemm_packed_a_fused_f32": (C.c_int, [_vp, _f32, _vp, _REF, _f32, _MUT, _BIAS, _i32, _f32,
+                                             _u32]),
+    "gk_gemm_packed_a_fused_bf16": (C.c_int, [_vp, _u16, _vp, _REF, _u16, _MUT, _BIAS, _i32,
+                                              _u16, _u32]),
+    "gk_gemm_packed_a_fused_f32_unchecked": (C.c_int, [_vp, _f32, _vp, _size, _vp, _sdiff, _sdiff,
+                                                       _f32, _vp, _sdiff, _sdiff, _vp, _i32, _u8,
+                                                       _i32, _f32, _u32]),
+    "gk_gemm_packed_a_fused_bf16_unchecked": (C.c_int, [_vp, _u16, _vp, _size, _vp, _sdiff,
+                                                        _sdiff, _u16, _vp, _sdiff, _sdiff, _vp,
+                                                        _i32, _u8, _i32, _u16, _u32]),
     "gk_gemm_packed_b_f32": (C.c_int, [_vp, _f32, _REF, _vp, _f32, _MUT, _u32]),
     "gk_gemm_packed_b_f32_unchecked": (C.c_int, [_vp, _f32, _size, _vp, _sdiff, _sdiff, _vp,
                                                  _f32, _vp, _sdiff, _sdiff, _u32]),

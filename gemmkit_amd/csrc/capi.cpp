@@ -220,6 +220,13 @@ struct gk_packed_rhs {
     int64_t ld = 0;                  // row stride in elements
 };
 
+struct gk_packed_lhs {
+    gk::InType in = gk::InType::F32;  // element type (PackedLhs<T>'s T)
+    void *buf = nullptr;              // m x ld, k-contiguous rows of A, zero padded
+    size_t m = 0, k = 0;
+    int64_t ld = 0;                   // row stride in elements
+};
+
 namespace {
 
 thread_local gk_workspace *tl_ws = nullptr;
@@ -473,7 +480,8 @@ int choose_splits(int64_t M, int64_t N, int64_t k, size_t esz) {
 int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t k, int64_t n,
                 const void *a, int64_t rsa, int64_t csa, int64_t bsa, const void *b,
                 int64_t rsb, int64_t csb, int64_t bsb, void *c, int64_t rsc, int64_t csc,
-                int64_t bsc, int64_t batch, const gk_packed_rhs *packed = nullptr) {
+                int64_t bsc, int64_t batch, const gk_packed_rhs *packed = nullptr,
+                const gk_packed_lhs *packed_a = nullptr) {
     const size_t esz = in_size(in);
     // Orientation: the kernels write C row-major-ish (kernel column index the
     // fast one), so a column-major-ish C computes C^T = B^T A^T -- a swap of
@@ -482,6 +490,7 @@ int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t
     Opnd A{a, rsa, csa, bsa};
     Opnd Bt{b, csb, rsb, bsb};  // B^T: n x k
     if (packed) Bt = Opnd{packed->buf, packed->ld, 1, 0};
+    if (packed_a) A = Opnd{packed_a->buf, packed_a->ld, 1, 0};
     int64_t M = m, N = n;
     ep.c = c;
     ep.bsc = bsc;
@@ -733,7 +742,7 @@ int exec_float(gk_workspace *ws, InType in, EpiKind kind, size_t batch, size_t m
                size_t n, float alpha, const void *a, ptrdiff_t rsa, ptrdiff_t csa, ptrdiff_t bsa,
                const void *b, ptrdiff_t rsb, ptrdiff_t csb, ptrdiff_t bsb, float beta, void *c,
                ptrdiff_t rsc, ptrdiff_t csc, ptrdiff_t bsc, const FusedSpec *fx = nullptr,
-               const gk_packed_rhs *packed = nullptr) {
+               const gk_packed_rhs *packed = nullptr, const gk_packed_lhs *packed_a = nullptr) {
     int r;
     if ((r = device_init())) return r;
     if (fx && (r = check_fused_enums(*fx))) return r;
@@ -758,7 +767,7 @@ int exec_float(gk_workspace *ws, InType in, EpiKind kind, size_t batch, size_t m
         return finish("fused fill");
     }
     return run_product(ws, in, ep, m, k, n, a, rsa, csa, bsa, b, rsb, csb, bsb, c, rsc, csc, bsc,
-                       batch, packed);
+                       batch, packed, packed_a);
 }
 
 // ---- requant core (execute_int_requant, src/dispatch/int.rs:672-700)
@@ -1134,6 +1143,111 @@ int packed_b_checked(gk_workspace *ws, InType in, EpiKind kind, size_t esz, floa
     const bool any = fused && (bias || act != GK_ACT_NONE);
     if (any && (r = lower_fused(bias, act, slope, a->rows, packed->n, c, esz, esz, &fx))) return r;
     return packed_b_unchecked(ws, in, kind, alpha, a->rows, a->data, a->rs, a->cs, packed, beta,
+                              c->data, c->rs, c->cs, any ? &fx : nullptr);
+}
+
+// ---- prepacked LHS (src/api/packed.rs:953-1527)
+
+int check_packed_lhs(const gk_packed_lhs *p, InType want) {
+    if (!p) return fail(GK_ERR_ARG, "gemmkit: null packed LHS");
+    if (p->in != want)
+        return fail(GK_ERR_ARG, "gemmkit: packed LHS holds %s elements, this entry takes %s",
+                    in_name(p->in), in_name(want));
+    return GK_OK;
+}
+
+// prepack_lhs_unchecked (src/api/packed.rs:999-1030): the rows of A stored
+// k-contiguous in an owned device buffer, padded to 16 bytes with zeros.  The
+// reference packs the transposed product's RHS; its size-overflow message
+// names that k x m RHS, and so does this one.
+int prepack_lhs_any(InType in, const void *a, ptrdiff_t rsa, ptrdiff_t csa, size_t m, size_t k,
+                    gk_packed_lhs **out) {
+    int r;
+    if (!out) return fail(GK_ERR_ARG, "gemmkit: null output handle");
+    *out = nullptr;
+    if ((r = device_init())) return r;
+    if (!dims_fit(m, k, 1, 1))
+        return fail(GK_ERR_OVERFLOW,
+                    "gemmkit: prepacked RHS of %zux%zu is too large; the pack buffer size "
+                    "overflows usize",
+                    k, m);
+    const int64_t esz = (int64_t)in_size(in);
+    gk_packed_lhs *p = new gk_packed_lhs();
+    p->in = in;
+    p->m = m;
+    p->k = k;
+    p->ld = round_up64(std::max<int64_t>((int64_t)k, 1), 16 / esz);
+    if (k > 0 && m > 0) {
+        size_t bytes = (size_t)p->ld * m * (size_t)esz;
+        hipError_t e = hipMalloc(&p->buf, bytes);
+        if (e != hipSuccess) {
+            delete p;
+            return fail(GK_ERR_NOMEM, "gemmkit: prepacked LHS allocation of %zu bytes failed", bytes);
+        }
+        e = launch_pack(in, a, rsa, csa, (int64_t)m, (int64_t)k, p->buf, p->ld, tl_stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(tl_stream);
+        if (e != hipSuccess) {
+            (void)hipFree(p->buf);
+            delete p;
+            return hip_fail(e, "prepack");
+        }
+    }
+    *out = p;
+    return ok();
+}
+
+// gemm_packed_a_unchecked_with's orientation assert (src/api/packed.rs:1190-1194).
+int check_packed_a_c_layout(ptrdiff_t rsc, ptrdiff_t csc) {
+    if (iabs64(csc) > iabs64(rsc))
+        return fail(GK_ERR_LAYOUT,
+                    "gemmkit: gemm_packed_a requires row-major-ish C (|csc| <= |rsc|); a "
+                    "column-major C would keep A in the LHS role and invalidate the prepacked LHS "
+                    "\xE2\x80\x94 use gemm() for that layout");
+    return GK_OK;
+}
+
+int packed_a_unchecked(gk_workspace *ws, InType in, EpiKind kind, float alpha,
+                       const gk_packed_lhs *packed, size_t n, const void *b, ptrdiff_t rsb,
+                       ptrdiff_t csb, float beta, void *c, ptrdiff_t rsc, ptrdiff_t csc,
+                       const FusedSpec *fx) {
+    int r;
+    if ((r = check_packed_lhs(packed, in))) return r;
+    if ((r = check_packed_a_c_layout(rsc, csc))) return r;
+    return exec_float(ws, in, kind, 1, packed->m, packed->k, n, alpha, nullptr, 0, 0, 0, b, rsb,
+                      csb, 0, beta, c, rsc, csc, 0, fx, nullptr, packed);
+}
+
+// gemm_packed_a_with / gemm_packed_a_fused_with's checks (src/api/packed.rs:1074-1107,
+// :1284-1325).
+int packed_a_checked(gk_workspace *ws, InType in, EpiKind kind, size_t esz, float alpha,
+                     const gk_packed_lhs *packed, const gk_mat_ref *b, float beta,
+                     const gk_mat_mut *c, bool fused, const gk_bias *bias, int32_t act,
+                     float slope) {
+    int r;
+    if (fused && (r = check_act_value(act))) return r;
+    if (!b || !c || !packed) return fail(GK_ERR_ARG, "gemmkit: null argument");
+    if (packed->k != b->rows)
+        return fail(GK_ERR_SHAPE, "gemmkit: packed A.cols (%zu) != B.rows (%zu)", packed->k,
+                    b->rows);
+    if (packed->m != c->rows)
+        return fail(GK_ERR_SHAPE, "gemmkit: packed A.rows (%zu) != C.rows (%zu)", packed->m,
+                    c->rows);
+    if (b->cols != c->cols)
+        return fail(GK_ERR_SHAPE, "gemmkit: B.cols (%zu) != C.cols (%zu)", b->cols, c->cols);
+    if ((r = check_view(b->len, b->rows, b->cols, b->rs, b->cs, "B"))) return r;
+    if ((r = check_view(c->len, c->rows, c->cols, c->rs, c->cs, "C"))) return r;
+    if (self_aliases(c->rows, c->cols, c->rs, c->cs))
+        return fail(GK_ERR_ALIAS,
+                    "gemmkit: C view aliases itself (strides %td,%td map distinct elements to the "
+                    "same memory); C must address each (i,j) uniquely",
+                    c->rs, c->cs);
+    if (overlaps_bytes(c->data, c->len, esz, b->data, b->len, esz))
+        return fail(GK_ERR_ALIAS, "gemmkit: C aliases B");
+    if ((r = check_packed_lhs(packed, in))) return r;
+    FusedSpec fx;
+    const bool any = fused && (bias || act != GK_ACT_NONE);
+    if (any && (r = lower_fused(bias, act, slope, packed->m, b->cols, c, esz, esz, &fx))) return r;
+    return packed_a_unchecked(ws, in, kind, alpha, packed, b->cols, b->data, b->rs, b->cs, beta,
                               c->data, c->rs, c->cs, any ? &fx : nullptr);
 }
 
@@ -1633,6 +1747,107 @@ int gk_gemm_packed_b_bf16(gk_workspace *ws, gk_bf16 alpha, const gk_mat_ref *a,
                           const gk_packed_rhs *packed, gk_bf16 beta, const gk_mat_mut *c, gk_par) {
     return packed_b_checked(ws, InType::BF16, EpiKind::BF16, 2, bf16_to_f32(alpha), a, packed,
                             bf16_to_f32(beta), c, false, nullptr, GK_ACT_NONE, 0.0f);
+}
+
+// ---- prepacked LHS (src/api/packed.rs:953-1527)
+
+int gk_prepack_lhs_f32_unchecked(const float *a, ptrdiff_t rsa, ptrdiff_t csa, size_t m, size_t k,
+                                 gk_packed_lhs **out) {
+    return prepack_lhs_any(InType::F32, a, rsa, csa, m, k, out);
+}
+
+int gk_prepack_lhs_f32(const gk_mat_ref *a, gk_packed_lhs **out) {
+    if (!a) return fail(GK_ERR_ARG, "gemmkit: null view argument");
+    int r = check_view(a->len, a->rows, a->cols, a->rs, a->cs, "A");
+    if (r) return r;
+    return prepack_lhs_any(InType::F32, a->data, a->rs, a->cs, a->rows, a->cols, out);
+}
+
+int gk_prepack_lhs_bf16_unchecked(const gk_bf16 *a, ptrdiff_t rsa, ptrdiff_t csa, size_t m,
+                                  size_t k, gk_packed_lhs **out) {
+    return prepack_lhs_any(InType::BF16, a, rsa, csa, m, k, out);
+}
+
+int gk_prepack_lhs_bf16(const gk_mat_ref *a, gk_packed_lhs **out) {
+    if (!a) return fail(GK_ERR_ARG, "gemmkit: null view argument");
+    int r = check_view(a->len, a->rows, a->cols, a->rs, a->cs, "A");
+    if (r) return r;
+    return prepack_lhs_any(InType::BF16, a->data, a->rs, a->cs, a->rows, a->cols, out);
+}
+
+void gk_packed_lhs_free(gk_packed_lhs *p) {
+    if (!p) return;
+    if (p->buf) {
+        (void)hipDeviceSynchronize();
+        (void)hipFree(p->buf);
+    }
+    delete p;
+}
+
+size_t gk_packed_lhs_rows(const gk_packed_lhs *p) { return p ? p->m : 0; }
+size_t gk_packed_lhs_cols(const gk_packed_lhs *p) { return p ? p->k : 0; }
+
+int gk_gemm_packed_a_f32_unchecked(gk_workspace *ws, float alpha, const gk_packed_lhs *packed,
+                                   size_t n, const float *b, ptrdiff_t rsb, ptrdiff_t csb,
+                                   float beta, float *c, ptrdiff_t rsc, ptrdiff_t csc, gk_par) {
+    return packed_a_unchecked(ws, InType::F32, EpiKind::F32, alpha, packed, n, b, rsb, csb, beta,
+                              c, rsc, csc, nullptr);
+}
+
+int gk_gemm_packed_a_f32(gk_workspace *ws, float alpha, const gk_packed_lhs *packed,
+                         const gk_mat_ref *b, float beta, const gk_mat_mut *c, gk_par) {
+    return packed_a_checked(ws, InType::F32, EpiKind::F32, 4, alpha, packed, b, beta, c, false,
+                            nullptr, GK_ACT_NONE, 0.0f);
+}
+
+int gk_gemm_packed_a_bf16_unchecked(gk_workspace *ws, gk_bf16 alpha, const gk_packed_lhs *packed,
+                                    size_t n, const gk_bf16 *b, ptrdiff_t rsb, ptrdiff_t csb,
+                                    gk_bf16 beta, gk_bf16 *c, ptrdiff_t rsc, ptrdiff_t csc,
+                                    gk_par) {
+    return packed_a_unchecked(ws, InType::BF16, EpiKind::BF16, bf16_to_f32(alpha), packed, n, b,
+                              rsb, csb, bf16_to_f32(beta), c, rsc, csc, nullptr);
+}
+
+int gk_gemm_packed_a_bf16(gk_workspace *ws, gk_bf16 alpha, const gk_packed_lhs *packed,
+                          const gk_mat_ref *b, gk_bf16 beta, const gk_mat_mut *c, gk_par) {
+    return packed_a_checked(ws, InType::BF16, EpiKind::BF16, 2, bf16_to_f32(alpha), packed, b,
+                            bf16_to_f32(beta), c, false, nullptr, GK_ACT_NONE, 0.0f);
+}
+
+int gk_gemm_packed_a_fused_f32(gk_workspace *ws, float alpha, const gk_packed_lhs *packed,
+                               const gk_mat_ref *b, float beta, const gk_mat_mut *c,
+                               const gk_bias *bias, int32_t act, float slope, gk_par) {
+    return packed_a_checked(ws, InType::F32, EpiKind::F32, 4, alpha, packed, b, beta, c, true,
+                            bias, act, slope);
+}
+
+int gk_gemm_packed_a_fused_bf16(gk_workspace *ws, gk_bf16 alpha, const gk_packed_lhs *packed,
+                                const gk_mat_ref *b, gk_bf16 beta, const gk_mat_mut *c,
+                                const gk_bias *bias, int32_t act, gk_bf16 slope, gk_par) {
+    return packed_a_checked(ws, InType::BF16, EpiKind::BF16, 2, bf16_to_f32(alpha), packed, b,
+                            bf16_to_f32(beta), c, true, bias, act, bf16_to_f32(slope));
+}
+
+int gk_gemm_packed_a_fused_f32_unchecked(gk_workspace *ws, float alpha,
+                                         const gk_packed_lhs *packed, size_t n, const float *b,
+                                         ptrdiff_t rsb, ptrdiff_t csb, float beta, float *c,
+                                         ptrdiff_t rsc, ptrdiff_t csc, const float *bias,
+                                         int32_t bias_dim, uint8_t has_bias, int32_t act,
+                                         float slope, gk_par) {
+    const FusedSpec fx{has_bias ? bias : nullptr, bias_dim, act, slope};
+    return packed_a_unchecked(ws, InType::F32, EpiKind::F32, alpha, packed, n, b, rsb, csb, beta,
+                              c, rsc, csc, &fx);
+}
+
+int gk_gemm_packed_a_fused_bf16_unchecked(gk_workspace *ws, gk_bf16 alpha,
+                                          const gk_packed_lhs *packed, size_t n,
+                                          const gk_bf16 *b, ptrdiff_t rsb, ptrdiff_t csb,
+                                          gk_bf16 beta, gk_bf16 *c, ptrdiff_t rsc, ptrdiff_t csc,
+                                          const gk_bf16 *bias, int32_t bias_dim,
+                                          uint8_t has_bias, int32_t act, gk_bf16 slope, gk_par) {
+    const FusedSpec fx{has_bias ? bias : nullptr, bias_dim, act, bf16_to_f32(slope)};
+    return packed_a_unchecked(ws, InType::BF16, EpiKind::BF16, bf16_to_f32(alpha), packed, n, b,
+                              rsb, csb, bf16_to_f32(beta), c, rsc, csc, &fx);
 }
 
 // ---- fused bias / activation (src/api/fused.rs, src/api/batched.rs:307-590,

@@ -521,6 +521,64 @@ int gk_gemm_packed_b_fused_bf16_unchecked(gk_workspace *ws, gk_bf16 alpha, size_
                                           int32_t bias_dim, uint8_t has_bias, int32_t act,
                                           gk_bf16 slope, gk_par par);
 
+/* ---------------------------------------------------- prepacked float LHS */
+
+/* PackedLhs<T> (src/api/packed.rs:953-981): an opaque, read-only device copy
+ * of A (m x k) in the kernels' k-contiguous row layout, for f32 or bf16;
+ * released with gk_packed_lhs_free. */
+typedef struct gk_packed_lhs gk_packed_lhs;
+
+/* prepack_lhs (src/api/packed.rs:986) / prepack_lhs_unchecked (:999). */
+int gk_prepack_lhs_f32(const gk_mat_ref *a, gk_packed_lhs **out);
+int gk_prepack_lhs_f32_unchecked(const float *a, ptrdiff_t rsa, ptrdiff_t csa, size_t m,
+                                 size_t k, gk_packed_lhs **out);
+int gk_prepack_lhs_bf16(const gk_mat_ref *a, gk_packed_lhs **out);
+int gk_prepack_lhs_bf16_unchecked(const gk_bf16 *a, ptrdiff_t rsa, ptrdiff_t csa, size_t m,
+                                  size_t k, gk_packed_lhs **out);
+void gk_packed_lhs_free(gk_packed_lhs *p);
+/* PackedLhs::rows / cols (src/api/packed.rs:963-973). */
+size_t gk_packed_lhs_rows(const gk_packed_lhs *p);
+size_t gk_packed_lhs_cols(const gk_packed_lhs *p);
+
+/* gemm_packed_a / _with (src/api/packed.rs:1049, :1065): C <- alpha*A*B +
+ * beta*C with the prepacked A, bit-identical to gemm; like the reference it
+ * requires a row-major-ish C (|csc| <= |rsc|). */
+int gk_gemm_packed_a_f32(gk_workspace *ws, float alpha, const gk_packed_lhs *packed,
+                         const gk_mat_ref *b, float beta, const gk_mat_mut *c, gk_par par);
+int gk_gemm_packed_a_bf16(gk_workspace *ws, gk_bf16 alpha, const gk_packed_lhs *packed,
+                          const gk_mat_ref *b, gk_bf16 beta, const gk_mat_mut *c, gk_par par);
+/* gemm_packed_a_unchecked(_with) (src/api/packed.rs:1143, :1174). */
+int gk_gemm_packed_a_f32_unchecked(gk_workspace *ws, float alpha, const gk_packed_lhs *packed,
+                                   size_t n, const float *b, ptrdiff_t rsb, ptrdiff_t csb,
+                                   float beta, float *c, ptrdiff_t rsc, ptrdiff_t csc,
+                                   gk_par par);
+int gk_gemm_packed_a_bf16_unchecked(gk_workspace *ws, gk_bf16 alpha, const gk_packed_lhs *packed,
+                                    size_t n, const gk_bf16 *b, ptrdiff_t rsb, ptrdiff_t csb,
+                                    gk_bf16 beta, gk_bf16 *c, ptrdiff_t rsc, ptrdiff_t csc,
+                                    gk_par par);
+/* gemm_packed_a_fused / _with (src/api/packed.rs:1250, :1272): the checks of
+ * gemm_packed_a plus the bias checks (bias in the user frame). */
+int gk_gemm_packed_a_fused_f32(gk_workspace *ws, float alpha, const gk_packed_lhs *packed,
+                               const gk_mat_ref *b, float beta, const gk_mat_mut *c,
+                               const gk_bias *bias, int32_t act, float slope, gk_par par);
+int gk_gemm_packed_a_fused_bf16(gk_workspace *ws, gk_bf16 alpha, const gk_packed_lhs *packed,
+                                const gk_mat_ref *b, gk_bf16 beta, const gk_mat_mut *c,
+                                const gk_bias *bias, int32_t act, gk_bf16 slope, gk_par par);
+/* gemm_packed_a_fused_unchecked(_with) (src/api/packed.rs:1369, :1406). */
+int gk_gemm_packed_a_fused_f32_unchecked(gk_workspace *ws, float alpha,
+                                         const gk_packed_lhs *packed, size_t n, const float *b,
+                                         ptrdiff_t rsb, ptrdiff_t csb, float beta, float *c,
+                                         ptrdiff_t rsc, ptrdiff_t csc, const float *bias,
+                                         int32_t bias_dim, uint8_t has_bias, int32_t act,
+                                         float slope, gk_par par);
+int gk_gemm_packed_a_fused_bf16_unchecked(gk_workspace *ws, gk_bf16 alpha,
+                                          const gk_packed_lhs *packed, size_t n,
+                                          const gk_bf16 *b, ptrdiff_t rsb, ptrdiff_t csb,
+                                          gk_bf16 beta, gk_bf16 *c, ptrdiff_t rsc, ptrdiff_t csc,
+                                          const gk_bf16 *bias, int32_t bias_dim,
+                                          uint8_t has_bias, int32_t act, gk_bf16 slope,
+                                          gk_par par);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif
