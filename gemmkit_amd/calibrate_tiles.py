@@ -108,6 +108,12 @@ def measure(out_path: str) -> None:
     add_bf("bf16_2048_bf16out", 2048, 2048, 2048, out="bf16")
     add_f32("f32_2048", 2048, 2048, 2048)
     add_f32("f32_1024", 1024, 1024, 1024)
+    # the rests a tail split launches (one short round of the CUs), and f32
+    # with many tiles
+    add_i8("i8_rest_q8", 2048, 2816, 4096, q8=True)
+    add_i8("i8_rest_i32", 2048, 2816, 4096)
+    add_bf("bf16_rest_bf16out", 2048, 2816, 4096, out="bf16")
+    add_f32("f32_4096x4096x1024", 4096, 4096, 1024)
     res = {}
     for name, (meta, fn) in cases.items():
         row = {}

@@ -353,31 +353,31 @@ bool skinny_enabled() {
 // flight).  A fraction `hide` of the epilogue and latency overlaps the next
 // tile's main loop when a CU runs more than one; the last is never hidden.
 // The constants are the fit of gemmkit_amd/calibrate_tiles.py to graph-timed
-// runs of 13 shapes x 8 tiles (int8 i32 and requantized, bf16 with f32 and
+// runs of 17 shapes x 8 tiles (int8 i32 and requantized, bf16 with f32 and
 // bf16 output, batched attention scores, f32; 1024^2 to 4096^3 and
 // 2048 x 11008 x 4096): least squares on log time, then refined so the chosen
 // tile is the best measured one on each shape.
 struct TileCand { Tile t; int bm, bn, occ; double eff[2], eff_i8, hide, epi, epi_q8; };
 static const TileCand kTileCands[] = {
-    {Tile::T256x256, 256, 256, 1, {0.876049, 0.876049}, 1.0, 0.446527, 1.0, 1.0},
-    {Tile::T256x256w8, 256, 256, 1, {0.905052, 0.905052}, 1.3, 0.397345, 1.141787, 0.935765},
-    {Tile::T256x128o2, 256, 128, 2, {0.773415, 0.583568}, 1.11073, 0.615115, 0.420867, 0.565076},
-    {Tile::T256x128, 256, 128, 1, {0.726001, 0.726001}, 1.064577, 0.208026, 0.311532, 0.901659},
-    {Tile::T128x128, 128, 128, 2, {0.787324, 0.532058}, 1.076563, 0.845232, 0.26268, 0.2},
-    {Tile::T64x64, 64, 64, 2, {0.814864, 0.441999}, 0.815275, 0.925765, 3.0, 2.140505},
-    {Tile::T256x256k128, 256, 256, 1, {0.891258, 0.891258}, 1.3, 0.327803, 1.0266, 1.143453},
-    {Tile::T256x256w8k128, 256, 256, 1, {0.907065, 0.907065}, 1.257551, 0.383056, 1.010608, 0.804656},
+    {Tile::T256x256, 256, 256, 1, {0.85303, 0.85303}, 1.0, 0.088032, 1.0, 1.0},
+    {Tile::T256x256w8, 256, 256, 1, {0.858816, 0.858816}, 1.121781, 5.3e-05, 0.94197, 0.728267},
+    {Tile::T256x128o2, 256, 128, 2, {0.666828, 0.618457}, 1.011653, 0.324247, 0.602712, 0.847837},
+    {Tile::T256x128, 256, 128, 1, {0.67676, 0.67676}, 1.026106, 0.0, 0.49797, 1.00419},
+    {Tile::T128x128, 128, 128, 2, {0.714723, 0.570162}, 0.974166, 0.826374, 1.166487, 0.4006},
+    {Tile::T64x64, 64, 64, 2, {0.493576, 0.455552}, 0.738895, 0.831829, 0.2, 0.2},
+    {Tile::T256x256k128, 256, 256, 1, {0.863509, 0.863509}, 1.3, 0.01624, 1.105762, 1.290751},
+    {Tile::T256x256w8k128, 256, 256, 1, {0.8647, 0.8647}, 0.988872, 0.00044, 0.746808, 0.344243},
 };
 
 // Model cost of running an M x N (x batch) product with tile c, in the units
 // of area / eff.
 double tile_cost(const TileCand &c, int64_t M, int64_t N, int64_t batch, int64_t kbytes,
                  EpiKind kind, InType in) {
-    const double c_epi = kind == EpiKind::Q8 ? 0.750473
-                         : kind == EpiKind::I32 ? 0.376841
-                         : kind == EpiKind::F32 ? 0.153472 : 0.0;
-    constexpr double kTileLatency = 19011.223;  // in the units of area / eff
-    constexpr double kF32Rate = 4.54331;    // f32 main-loop cost per K byte vs i8/bf16
+    const double c_epi = kind == EpiKind::Q8 ? 0.643382
+                         : kind == EpiKind::I32 ? 0.342823
+                         : kind == EpiKind::F32 ? 0.301602 : 0.0;
+    constexpr double kTileLatency = 13829.251;  // in the units of area / eff
+    constexpr double kF32Rate = 4.562511;    // f32 main-loop cost per K byte vs i8/bf16
     const double kf = (double)std::max<int64_t>(kbytes, 64) / 4096.0 *
                       (in == InType::F32 ? kF32Rate : 1.0);
     const int64_t cus = g_num_cus > 0 ? g_num_cus : 256;

@@ -89,7 +89,7 @@ def test_requant(dev, axis, u8):
 
 
 def test_bf16_fused_bias_relu(dev):
-    m, k, n = 2048, 2048, 8448
+    m, k, n = 2048, 4096, 11008
     assert gk.debug_plan("bf16", "bf16", m, n, 2 * k)[1] > 0
     g = torch.Generator().manual_seed(7)
     a = torch.randn(m * k, generator=g).to(torch.bfloat16).to(dev)
