@@ -275,18 +275,29 @@ static unsigned gemv_grid(int64_t groups, int cus, int per_cu) {
     return (unsigned)(blocks < 1 ? 1 : blocks);
 }
 
-// Rows per wave iteration: about 16 chunk loads per lane in flight behind the
-// arithmetic, at most 4 rows, and 2 when 8 vectors already fill the registers.
+// Rows per wave iteration and workgroups per CU, from a graph-timed sweep over
+// 1 KB..8 KB rows (i8, f32 and bf16, 4096..65536 rows, five rotating matrix
+// copies so the Infinity Cache cannot serve them).  Rows of 4 KB or more want
+// about 8 KB per wave iteration (2 rows of 4 KB, 1 of 8 KB) and 3 workgroups
+// per CU: on a 58.7 MB i8 matrix that is 10.2 us against 11.4 us for 4 rows
+// and up to 8 workgroups per CU, which keeps more bytes in flight but spends
+// longer in each wave's reduction and store before its next loads.  Shorter
+// rows keep 4 rows per iteration and up to 8 workgroups per CU.
 template <int NV, int CPL>
 constexpr int rows_per_wave() {
-    return (CPL >= 8 || (NV >= 8 && CPL >= 4)) ? 2 : 4;
+    return CPL >= 8 ? 1 : (CPL >= 4 ? 2 : 4);
+}
+
+template <int CPL>
+constexpr int reg_per_cu() {
+    return CPL >= 4 ? 3 : 8;
 }
 
 template <InType T, EpiKind E, int NV, int CPL>
 static hipError_t go_reg(const GemvArgs &g, const EpiParams &ep, hipStream_t stream) {
     constexpr int RPW = rows_per_wave<NV, CPL>();
     const int64_t groups = ((int64_t)g.R + RPW - 1) / RPW;
-    hipLaunchKernelGGL((gemv_reg<T, E, NV, CPL, RPW>), dim3(gemv_grid(groups, g.cus, 8)),
+    hipLaunchKernelGGL((gemv_reg<T, E, NV, CPL, RPW>), dim3(gemv_grid(groups, g.cus, reg_per_cu<CPL>())),
                        dim3(kGemvThreads), 0, stream, g, ep);
     return hipGetLastError();
 }
