@@ -341,6 +341,20 @@ bool skinny_enabled() {
     return !(s && !strcmp(s, "0"));
 }
 
+// Short sides where the wavefront GEMV streams faster than the matrix-core
+// skinny kernel (graph-timed on 14336-row weights, five rotating copies):
+// i8 with 2 vectors and 2..8 KiB rows (14336x4096: 11.1 against 12.7 us),
+// f32 with 2..4 vectors and 4..8 KiB rows, where the skinny kernel spends
+// four matrix-core operations per 16-byte chunk (14336x1024, 2 vectors:
+// 11.0 against 18.4 us; 3 vectors: 14.0 against 17.8 us).  bf16 ties or
+// loses.  Taken only when both operands are k-contiguous already, so the
+// GEMV needs no pack launch.
+static bool gemv_beats_skinny(InType in, int64_t short_side, int64_t kbytes) {
+    if (in == InType::I8) return short_side == 2 && kbytes >= 2048 && kbytes <= 8192;
+    if (in == InType::F32) return short_side <= 4 && kbytes >= 4096 && kbytes <= 8192;
+    return false;
+}
+
 // Tile choice: the tile with the smallest makespan.  Tiles spread evenly over
 // the CUs, so the busiest CU runs per_cu = ceil(tiles / CUs) of them, up to
 // `occ` at a time.  A tile costs its main loop, BM*BN*kf / eff (kf: K bytes
@@ -521,9 +535,11 @@ int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t
     // streams best with the wavefront GEMV (a whole 1 KiB row segment per
     // load, no cross-wave exchange); 2..16 vectors go to the matrix-core
     // skinny kernel, which stages the vectors from any strides itself (only
-    // the long operand must be k-contiguous).
+    // the long operand must be k-contiguous), except the few short sides
+    // gemv_beats_skinny names.
     const bool vec_is_a = M <= N;
-    const bool skinny_ok = short_side >= 2 && short_side <= 16 && skinny_enabled() && k_fits &&
+    const bool gemv_first = a_ok && b_ok && gemv_beats_skinny(in, short_side, k * (int64_t)esz);
+    const bool skinny_ok = short_side >= 2 && short_side <= 16 && !gemv_first && skinny_enabled() && k_fits &&
                            (vec_is_a ? b_rs : a_rs) * (int64_t)esz <= kMaxTileRowBytes &&
                            skinny_lds_bytes(in, k, (int)short_side) <= kSkinnyLdsMax;
     const bool vector_route = skinny_ok || short_side <= 8;

@@ -53,10 +53,11 @@ def test_i8_skinny_layouts(dev, m, k, n, la, lb, lc):
     run_case(dev, m, k, n, 2, 1, la, lb, lc, seed=12)
 
 
-@pytest.mark.parametrize("m,k,n", [(2, 4096, 777), (8, 4096, 1000), (6, 4112, 300),
-                                   (500, 1040, 3)])
+@pytest.mark.parametrize("m,k,n", [(2, 1040, 777), (8, 4096, 1000), (6, 4112, 300),
+                                   (500, 1040, 3), (2, 4096, 777)])
 def test_i8_skinny_matches_gemv(dev, m, k, n):
-    """Both skinny kernels give identical bits (wrapping i32 sums)."""
+    """Both skinny kernels give identical bits (wrapping i32 sums); (2, 4096)
+    takes the wavefront GEMV on both runs (two vectors with 4 KiB rows)."""
     run_case(dev, m, k, n, 1, 0, "row", "col", "row", seed=13)
     with no_skinny():
         run_case(dev, m, k, n, 1, 0, "row", "col", "row", seed=13)
@@ -78,7 +79,9 @@ def test_decode_gemv_full_size(dev, m):
 
 
 @pytest.mark.parametrize("m,k,n", [(1, 5000, 300), (300, 5000, 1), (4, 1000, 513), (700, 64, 16),
-                                   (16, 2048, 200), (7, 3, 90)])
+                                   (16, 2048, 200), (7, 3, 90),
+                                   # 2..4 vectors with 4..8 KiB rows: the wavefront GEMV
+                                   (2, 1024, 700), (3, 2048, 301), (600, 1536, 4), (4, 2048, 64)])
 @pytest.mark.parametrize("alpha,beta", [(1.0, 0.0), (0.75, -1.5)])
 def test_f32_skinny(dev, m, k, n, alpha, beta):
     a = oracle.rand_vec(41 + m, m * k).astype(np.float32).reshape(m, k)
