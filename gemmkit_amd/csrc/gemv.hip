@@ -283,7 +283,7 @@ static unsigned gemv_grid(int64_t groups, int cus, int per_cu) {
 // and up to 8 workgroups per CU, which keeps more bytes in flight but spends
 // longer in each wave's reduction and store before its next loads.  Shorter
 // rows keep 4 rows per iteration and up to 8 workgroups per CU.
-template <int NV, int CPL>
+template <int CPL>
 constexpr int rows_per_wave() {
     return CPL >= 8 ? 1 : (CPL >= 4 ? 2 : 4);
 }
@@ -295,7 +295,7 @@ constexpr int reg_per_cu() {
 
 template <InType T, EpiKind E, int NV, int CPL>
 static hipError_t go_reg(const GemvArgs &g, const EpiParams &ep, hipStream_t stream) {
-    constexpr int RPW = rows_per_wave<NV, CPL>();
+    constexpr int RPW = rows_per_wave<CPL>();
     const int64_t groups = ((int64_t)g.R + RPW - 1) / RPW;
     hipLaunchKernelGGL((gemv_reg<T, E, NV, CPL, RPW>), dim3(gemv_grid(groups, g.cus, reg_per_cu<CPL>())),
                        dim3(kGemvThreads), 0, stream, g, ep);
