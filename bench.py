@@ -25,6 +25,11 @@ roofline: algorithmic ops of one 4096^3 launch (2*4096^3) over the average
 launch time from the HIP events, against MI355X's published dense int8 peak
 (5.0 POP/s).  traffic: HBM bytes per launch from the committed rocprofv3
 counter summary (profiles/traffic.json), or null.
+mfma_util: the headline kernel's matrix-core utilisation from the committed
+rocprofv3 counter summary (profiles/mfma_util.json): SQ_VALU_MFMA_BUSY_CYCLES
+over GRBM_GUI_ACTIVE per XCD times the 1024 SIMDs, i.e. busy against the
+clock the chip ran at under the counters (eager launches), or null.  The
+roofline's frac is the same kernel against the published 2.4 GHz peak.
 cpu_baseline: the oracle's C restatement of gemmkit's CPU i8 path (BLIS
 5-loop + AVX-512 VNNI microkernel, OpenMP threads) on the host cores, timed
 the way gemmkit's perf harness times (3 warmups, ~70 ms batches, median of 9).
@@ -173,6 +178,15 @@ def main():
     if os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("i8_gemm_4096", {}).get("hbm_bytes_per_launch")
+    mfma_util = None
+    upath = os.path.join(ROOT, "profiles", "mfma_util.json")
+    if os.path.exists(upath):
+        with open(upath) as f:
+            u = json.load(f).get("i8_gemm_4096")
+        if u:
+            mfma_util = {"value": u["mfma_util"], "clock_ghz": u["clock_ghz"],
+                         "source": "rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD "
+                                   "x 1024 SIMDs), eager launches; profiles/mfma_util.json"}
     line = {
         "metric": "int8 GEMM TOPS + MFMA util at 4096³; bf16 TFLOPS; GEMV HBM GB/s",
         "value": value,
@@ -194,6 +208,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": value, "peak": PEAK["int8"] / 1e12,
                      "unit": "TOPS", "frac": (value * 1e12 / PEAK["int8"]) if value else None,
                      "traffic": traffic},
+        "mfma_util": mfma_util,
         "cpu_baseline": cpu,
         "workloads": workloads,
     }
