@@ -37,6 +37,8 @@ I8_CASES = [
     (1, 16, 1), (1, 64, 100), (2, 48, 33), (3, 1040, 31), (5, 4096, 1000), (8, 100, 257),
     (9, 4096, 64), (12, 640, 129), (16, 4112, 300), (16, 16, 16),
     (100, 64, 1), (257, 48, 2), (1000, 4096, 7), (33, 1040, 12), (300, 4112, 16),
+    # one vector, 1..8 KiB rows (4, 4, 2 and 1 rows per wave iteration), ragged row counts
+    (1, 1024, 257), (1, 2048, 1001), (1, 4096, 3), (1, 8192, 301), (1001, 8192, 1),
 ]
 
 
@@ -81,7 +83,9 @@ def test_decode_gemv_full_size(dev, m):
 @pytest.mark.parametrize("m,k,n", [(1, 5000, 300), (300, 5000, 1), (4, 1000, 513), (700, 64, 16),
                                    (16, 2048, 200), (7, 3, 90),
                                    # 2..4 vectors with 4..8 KiB rows: the wavefront GEMV
-                                   (2, 1024, 700), (3, 2048, 301), (600, 1536, 4), (4, 2048, 64)])
+                                   (2, 1024, 700), (3, 2048, 301), (600, 1536, 4), (4, 2048, 64),
+                                   # one vector, 4 and 8 KiB rows, ragged row counts
+                                   (1, 1024, 3), (1, 2048, 257), (513, 2048, 1)])
 @pytest.mark.parametrize("alpha,beta", [(1.0, 0.0), (0.75, -1.5)])
 def test_f32_skinny(dev, m, k, n, alpha, beta):
     a = oracle.rand_vec(41 + m, m * k).astype(np.float32).reshape(m, k)
