@@ -65,11 +65,17 @@ def parse():
 
 class Timer:
     """Times `steps` calls of `fn` (a list of callables cycled in order) on the
-    current stream: captured into a HIP graph and replayed, or eager."""
+    current stream: captured into a HIP graph and replayed `replays` times,
+    each replay bracketed by HIP events on that stream, or eager.  Returns the
+    median per-call time over the replays; `last` keeps the min and max (the
+    reference's harness reports the median with its spread,
+    tests/perf/harness.rs:62-120)."""
 
-    def __init__(self, eager: bool, warmup_ms: float):
+    def __init__(self, eager: bool, warmup_ms: float, replays: int = 7):
         self.eager = eager
         self.warmup_ms = warmup_ms
+        self.replays = max(1, replays)
+        self.last = {}
 
     def __call__(self, fns, steps: int, warmup: int) -> float:
         import torch
@@ -89,28 +95,36 @@ class Timer:
         stream = torch.cuda.current_stream()
         start = torch.cuda.Event(enable_timing=True)
         stop = torch.cuda.Event(enable_timing=True)
+        times = []
         if self.eager:
-            start.record(stream)
-            for i in range(steps):
-                fns[i % len(fns)]()
-            stop.record(stream)
-            torch.cuda.synchronize()
-            return start.elapsed_time(stop) / steps
-        graph = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream()
-        side.wait_stream(stream)
-        with torch.cuda.stream(side):
-            with torch.cuda.graph(graph, stream=side):
+            for _ in range(self.replays):
+                start.record(stream)
                 for i in range(steps):
                     fns[i % len(fns)]()
-        stream.wait_stream(side)
-        graph.replay()  # untimed replay: first-launch costs
-        torch.cuda.synchronize()
-        start.record(stream)
-        graph.replay()
-        stop.record(stream)
-        torch.cuda.synchronize()
-        return start.elapsed_time(stop) / steps
+                stop.record(stream)
+                torch.cuda.synchronize()
+                times.append(start.elapsed_time(stop) / steps)
+        else:
+            graph = torch.cuda.CUDAGraph()
+            side = torch.cuda.Stream()
+            side.wait_stream(stream)
+            with torch.cuda.stream(side):
+                with torch.cuda.graph(graph, stream=side):
+                    for i in range(steps):
+                        fns[i % len(fns)]()
+            stream.wait_stream(side)
+            graph.replay()  # untimed replay: first-launch costs
+            torch.cuda.synchronize()
+            for _ in range(self.replays):
+                start.record(stream)
+                graph.replay()
+                stop.record(stream)
+                torch.cuda.synchronize()
+                times.append(start.elapsed_time(stop) / steps)
+        times.sort()
+        med = times[len(times) // 2]
+        self.last = {"ms_min": times[0], "ms_max": times[-1], "replays": len(times)}
+        return med
 
 
 def main():
@@ -153,7 +167,7 @@ def main():
     if want("i8_gemm_4096"):
         call = lambda: gk.gemm_i8_unchecked(M, K, N, 1, ad, K, 1, bd, 1, K, 0, cd, N, 1)  # noqa: E731
         i8_ms = timed(call, args.steps, args.warmup)
-        entry = {"ms": i8_ms, "TOPS": 2 * M * N * K / i8_ms / 1e9}
+        entry = {"ms": i8_ms, "TOPS": 2 * M * N * K / i8_ms / 1e9, **timed.last}
         if need_oracle:
             # spot check the timed output: row 17 against the oracle
             ref = np.zeros(N, np.int32)
@@ -236,7 +250,7 @@ def run_extras(args, workloads, want, timed, dev, gk, np, torch):
             T, x, K, 1, packed, 0.0, scale, 0, bias, y, Nc, 1, axis=1, relu=True)
         ms = timed(call, 16 * max(1, steps // 8), 2)
         ops = 2 * T * K * Nc
-        workloads["i8_layer_requant"] = {"ms_per_call": ms, "calls_per_step": 16,
+        workloads["i8_layer_requant"] = {"ms_per_call": ms, "calls_per_step": 16, **timed.last,
                                          "TOPS": ops / ms / 1e9,
                                          "frac_int8_peak": ops / (ms * 1e-3) / 5.0e15}
         del x, w, y, packed
@@ -253,7 +267,8 @@ def run_extras(args, workloads, want, timed, dev, gk, np, torch):
             0.0, gk.MatMut.from_row_major(out, S, S), S * S)
         ms = timed(call, steps, warm)
         byts = 2 * Bt * S * D * 2 + Bt * S * S * 4
-        workloads["bf16_batched_attn"] = {"ms": ms, "TFLOPS": 2 * Bt * S * S * D / ms / 1e9,
+        workloads["bf16_batched_attn"] = {"ms": ms, **timed.last,
+                                          "TFLOPS": 2 * Bt * S * S * D / ms / 1e9,
                                           "GBps": byts / ms / 1e6,
                                           "frac_hbm": byts / (ms * 1e-3) / 8.0e12}
         del q, kk, out
@@ -268,7 +283,7 @@ def run_extras(args, workloads, want, timed, dev, gk, np, torch):
                                            gk.MatRef(b, n, n, 1, n), 0.0,
                                            gk.MatMut.from_row_major(c, n, n))
         ms = timed(call, steps, warm)
-        workloads["bf16_gemm_4096"] = {"ms": ms, "TFLOPS": 2 * n ** 3 / ms / 1e9,
+        workloads["bf16_gemm_4096"] = {"ms": ms, **timed.last, "TFLOPS": 2 * n ** 3 / ms / 1e9,
                                        "frac_bf16_peak": 2 * n ** 3 / (ms * 1e-3) / 2.5e15}
         del a, b, c
 
@@ -283,7 +298,7 @@ def run_extras(args, workloads, want, timed, dev, gk, np, torch):
                      for w in copies]
             ms = timed(calls, 10 * len(calls), warm)
             byts = Nw * K + Mv * K + Mv * Nw * 4
-            workloads[f"i8_gemv_m{Mv}"] = {"ms": ms, "GBps": byts / ms / 1e6,
+            workloads[f"i8_gemv_m{Mv}"] = {"ms": ms, **timed.last, "GBps": byts / ms / 1e6,
                                            "frac_hbm": byts / (ms * 1e-3) / 8.0e12}
         del copies
 
@@ -296,7 +311,7 @@ def run_extras(args, workloads, want, timed, dev, gk, np, torch):
         call = lambda: gk.gemm_unchecked(n, n, 1, 1.0, A, n, 1, xv, 1, 1, 0.0, yv, 1, 1)  # noqa: E731
         ms = timed(call, steps, warm)
         byts = n * n * 4 + n * 4 + n * 4
-        workloads["f32_gemv_16384"] = {"ms": ms, "GBps": byts / ms / 1e6,
+        workloads["f32_gemv_16384"] = {"ms": ms, **timed.last, "GBps": byts / ms / 1e6,
                                        "frac_hbm": byts / (ms * 1e-3) / 8.0e12}
         del A
 
@@ -308,7 +323,7 @@ def run_extras(args, workloads, want, timed, dev, gk, np, torch):
         c = torch.empty(n * n, device=dev)
         call = lambda: gk.gemm_unchecked(n, n, n, 1.0, a, n, 1, b, n, 1, 0.0, c, n, 1)  # noqa: E731
         ms = timed(call, steps, warm)
-        workloads["f32_gemm_512"] = {"ms": ms, "TFLOPS": 2 * n ** 3 / ms / 1e9}
+        workloads["f32_gemm_512"] = {"ms": ms, **timed.last, "TFLOPS": 2 * n ** 3 / ms / 1e9}
 
     # bf16 4096^3 with bf16 output: plain, and fused with a per-column bias and
     # ReLU (the epilogue's cost is the difference)

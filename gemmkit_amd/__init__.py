@@ -152,6 +152,18 @@ class Workspace:
         self._free = L.gk_workspace_free  # held so __del__ works during interpreter exit
         self._h = L.gk_workspace_new()
 
+    @classmethod
+    def with_capacity(cls, nbytes: int) -> "Workspace":
+        """Workspace::with_capacity (src/workspace.rs:78): the arena allocated up
+        front, so later calls (also under HIP graph capture) need not grow it."""
+        L = _lib.lib()
+        ws = cls.__new__(cls)
+        ws._free = L.gk_workspace_free
+        ws._h = L.gk_workspace_with_capacity(int(nbytes))
+        if not ws._h:
+            raise MemoryError(f"gemmkit: workspace allocation of {nbytes} bytes failed")
+        return ws
+
     @property
     def handle(self):
         return self._h
@@ -584,19 +596,24 @@ def gemm_batched_slice(problems, par: Optional[Parallelism] = None,
 
 
 def gemm_batched_unchecked(batch, m, k, n, alpha, a, rsa, csa, a_bs, b, rsb, csb, b_bs, beta,
-                           c, rsc, csc, c_bs, par=None, ws=None) -> None:
-    """``gemm_batched_unchecked(_with)`` (src/api/batched.rs:594-700)."""
+                           c, rsc, csc, c_bs, par=None, ws=None, a_off=0, b_off=0,
+                           c_off=0) -> None:
+    """``gemm_batched_unchecked(_with)`` (src/api/batched.rs:594-700).
+
+    ``*_off`` are element offsets of the base pointers (negative strides and
+    batch strides walk backwards from there)."""
     _bind_stream()
     L = _lib.lib()
     if a.dtype == torch.float32:
-        _check(L.gk_gemm_batched_f32_unchecked(_ws(ws), batch, m, k, n, float(alpha), _ptr(a),
-                                               rsa, csa, a_bs, _ptr(b), rsb, csb, b_bs,
-                                               float(beta), _ptr(c), rsc, csc, c_bs, _par(par)))
+        _check(L.gk_gemm_batched_f32_unchecked(_ws(ws), batch, m, k, n, float(alpha),
+                                               _ptr(a, a_off), rsa, csa, a_bs, _ptr(b, b_off),
+                                               rsb, csb, b_bs, float(beta), _ptr(c, c_off), rsc,
+                                               csc, c_bs, _par(par)))
     elif a.dtype == torch.bfloat16:
         _check(L.gk_gemm_batched_bf16_unchecked(_ws(ws), batch, m, k, n, _bf16_bits(alpha),
-                                                _ptr(a), rsa, csa, a_bs, _ptr(b), rsb, csb, b_bs,
-                                                _bf16_bits(beta), _ptr(c), rsc, csc, c_bs,
-                                                _par(par)))
+                                                _ptr(a, a_off), rsa, csa, a_bs, _ptr(b, b_off),
+                                                rsb, csb, b_bs, _bf16_bits(beta),
+                                                _ptr(c, c_off), rsc, csc, c_bs, _par(par)))
     else:
         raise TypeError("gemmkit_amd: gemm_batched_unchecked supports float32 and bfloat16")
 

@@ -89,6 +89,7 @@ SIGNATURES: dict[str, tuple] = {
     "gk_get_stream": (_vp, []),
     "gk_set_synchronous": (C.c_int, [C.c_int]),
     "gk_workspace_new": (_vp, []),
+    "gk_workspace_with_capacity": (_vp, [_size]),
     "gk_workspace_free": (None, [_vp]),
     "gk_workspace_bytes": (_size, [_vp]),
     "gk_gemm_f32": (C.c_int, [_vp, _f32, _REF, _REF, _f32, _MUT, _u32]),

@@ -21,6 +21,9 @@
 #include <mutex>
 #include <string>
 
+#include <sys/syscall.h>
+#include <unistd.h>
+
 #include "../../include/gemmkit_hip.h"
 #include "internal.h"
 
@@ -229,17 +232,52 @@ struct gk_packed_lhs {
 
 namespace {
 
-thread_local gk_workspace *tl_ws = nullptr;
+// The calling thread's default workspace (the reference's thread-local pool,
+// src/workspace.rs:205-230): created on first use and released when a worker
+// thread exits.  The main thread's arena is left to the process teardown,
+// where the HIP runtime may already be gone.
+struct ThreadWs {
+    gk_workspace *ws = nullptr;
+    ~ThreadWs() {
+        if (!ws) return;
+        if (ws->ptr && (pid_t)syscall(SYS_gettid) != getpid()) {
+            (void)hipDeviceSynchronize();
+            (void)hipFree(ws->ptr);
+            ws->ptr = nullptr;
+        }
+        if (!ws->ptr) delete ws;
+    }
+};
+thread_local ThreadWs tl_ws;
 
 gk_workspace *resolve_ws(gk_workspace *ws) {
     if (ws) return ws;
-    if (!tl_ws) tl_ws = new gk_workspace();
-    return tl_ws;
+    if (!tl_ws.ws) tl_ws.ws = new gk_workspace();
+    return tl_ws.ws;
+}
+
+// True when the calling thread's launch stream is being captured into a HIP
+// graph: nothing may allocate, free or synchronize then.
+bool stream_capturing() {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(tl_stream, &st) != hipSuccess) return false;
+    return st != hipStreamCaptureStatusNone;
 }
 
 // Returns a device region of at least `bytes`, growing the arena when needed.
+// Growing synchronizes the device (work already queued may still read the old
+// arena) and reallocates, which graph capture does not allow: under capture a
+// call that needs more than the arena holds fails instead, and the caller
+// reserves the arena beforehand (gk_workspace_with_capacity, or one eager call
+// of the same shape).
 int ws_reserve(gk_workspace *ws, size_t bytes, void **out) {
     if (ws->bytes < bytes) {
+        if (stream_capturing())
+            return fail(GK_ERR_NOMEM,
+                        "gemmkit: the workspace must grow from %zu to %zu bytes during HIP graph "
+                        "capture, which cannot allocate; size it before capturing "
+                        "(gk_workspace_with_capacity, or one uncaptured call of the same shape)",
+                        ws->bytes, bytes);
         size_t want = std::max(bytes, ws->bytes + ws->bytes / 2);
         want = (want + 0xFFFFF) & ~(size_t)0xFFFFF;
         if (ws->ptr) {
@@ -282,10 +320,16 @@ struct Opnd {
     int64_t rs, ks, bs;
 };
 
+// k-contiguous and 16-byte aligned, so the kernels can read it in place.  The
+// kernels address a tile's rows as unsigned 32-bit offsets from its first row,
+// so a negative row stride (legal on the unchecked tier) is never canonical:
+// such an operand goes through the pack, which indexes in 64 bits.  A negative
+// batch stride is fine (the kernels form each element's base in 64 bits).
 bool canonical(const Opnd &o, int64_t R, int64_t K, size_t esz, int64_t batch) {
     if (K * (int64_t)esz % 16 != 0) return false;
     if (o.ks != 1 && K > 1) return false;
     if ((uintptr_t)o.p % 16 != 0) return false;
+    if (R > 1 && o.rs < 0) return false;
     if (R > 1 && (o.rs * (int64_t)esz) % 16 != 0) return false;
     if (batch > 1 && (o.bs * (int64_t)esz) % 16 != 0) return false;
     return true;
@@ -489,13 +533,192 @@ int choose_splits(int64_t M, int64_t N, int64_t k, size_t esz) {
                                   kMaxSplits);
 }
 
+// Device memory a call may use for packed operands and split-K partial sums:
+// the workspace arena (grown on demand), or a fixed region handed down (the
+// no-allocation entry point's static scratch, or the inner calls of a K-sliced
+// product).
+struct Region {
+    gk_workspace *ws;      // used when fixed == nullptr
+    uint8_t *fixed;
+    size_t fixed_bytes;
+};
+
+int region_get(const Region &rg, size_t bytes, uint8_t **out) {
+    if (rg.fixed) {
+        if (bytes > rg.fixed_bytes)
+            return fail(GK_ERR_NOMEM,
+                        "gemmkit: this call needs %zu bytes of device scratch but its fixed "
+                        "scratch holds %zu",
+                        bytes, rg.fixed_bytes);
+        *out = rg.fixed;
+        return GK_OK;
+    }
+    void *p = nullptr;
+    int r = ws_reserve(resolve_ws(rg.ws), bytes, &p);
+    if (r) return r;
+    *out = (uint8_t *)p;
+    return GK_OK;
+}
+
+int64_t out_size(EpiKind kind) {
+    return kind == EpiKind::Q8 ? 1 : (kind == EpiKind::BF16 ? 2 : 4);
+}
+
+const void *ptr_add(const void *p, int64_t bytes) {
+    return p ? (const void *)((const uint8_t *)p + bytes) : p;
+}
+
+// Moves the per-channel vectors of `ep` (requantization scales and biases, or
+// the fused bias) `off` channels on, when their axis is `axis`.
+void channel_shift(EpiParams &ep, int32_t axis, int64_t off) {
+    if (ep.axis != axis || off == 0) return;
+    if (ep.scales) ep.scales += off;
+    if (ep.bias) ep.bias += off;
+    if (ep.fbias) ep.fbias = (const uint8_t *)ep.fbias + off * (ep.kind == EpiKind::BF16 ? 2 : 4);
+}
+
+// Rows or columns of the kernel frame one launch covers (tile indices and
+// output coordinates are 32-bit in the kernels); longer sides run in pieces.
+constexpr int64_t kMaxSide = int64_t(1) << 30;
+// Partial-sum bytes of one split-K launch; a batch whose slabs need more runs
+// in chunks of elements.
+constexpr int64_t kSlabMax = int64_t(64) << 20;
+// K bytes per piece of a K-sliced product (a multiple of every stage size).
+constexpr int64_t kSliceBytes = int64_t(4) << 20;
+// Longest K the wavefront GEMV takes in one launch.
+constexpr int64_t kGemvMaxK = INT32_MAX;
+
+int run_fit(const Region &rg, InType in, EpiParams ep, int64_t m, int64_t k, int64_t n,
+            const void *a, int64_t rsa, int64_t csa, int64_t bsa, const void *b, int64_t rsb,
+            int64_t csb, int64_t bsb, void *c, int64_t rsc, int64_t csc, int64_t bsc,
+            int64_t batch, const gk_packed_rhs *packed, const gk_packed_lhs *packed_a);
+
 // The shared core: C = epi(A*B) for every batch element.  `ep` comes in the
 // user frame (rsc/csc of the user's C, axis 0 = per user row); m, k, n >= 1.
-int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t k, int64_t n,
+// Products larger than one launch takes are cut here, in the user frame, into
+// pieces that each run as the standalone product would:
+//   * more than kMaxGridZ batch elements: chunks of elements;
+//   * more than kMaxSide rows or columns: bands of rows or columns (their
+//     per-channel vectors move with them);
+//   * a K too long for the kernels' 32-bit row offsets: K slices of
+//     kSliceBytes whose products are summed in order into a native
+//     accumulator slab (wrapping i32, or f32) -- the reference's own kc
+//     slicing with beta = 1 after the first slice (src/driver.rs:725-730) --
+//     and one pass then applies the call's epilogue to the sum.
+int run_product(const Region &rg, InType in, EpiParams ep, int64_t m, int64_t k, int64_t n,
                 const void *a, int64_t rsa, int64_t csa, int64_t bsa, const void *b,
                 int64_t rsb, int64_t csb, int64_t bsb, void *c, int64_t rsc, int64_t csc,
                 int64_t bsc, int64_t batch, const gk_packed_rhs *packed = nullptr,
                 const gk_packed_lhs *packed_a = nullptr) {
+    const int64_t esz = (int64_t)in_size(in), osz = out_size(ep.kind);
+    int r;
+    if (batch > kMaxGridZ) {
+        for (int64_t z0 = 0; z0 < batch; z0 += kMaxGridZ) {
+            const int64_t nb = std::min(kMaxGridZ, batch - z0);
+            if ((r = run_product(rg, in, ep, m, k, n, ptr_add(a, z0 * bsa * esz), rsa, csa, bsa,
+                                 ptr_add(b, z0 * bsb * esz), rsb, csb, bsb,
+                                 (void *)ptr_add(c, z0 * bsc * osz), rsc, csc, bsc, nb, packed,
+                                 packed_a)))
+                return r;
+        }
+        return ok();
+    }
+    if (m > kMaxSide) {
+        for (int64_t i0 = 0; i0 < m; i0 += kMaxSide) {
+            const int64_t len = std::min(kMaxSide, m - i0);
+            EpiParams e = ep;
+            channel_shift(e, 0, i0);
+            gk_packed_lhs pa;
+            if (packed_a) {
+                pa = *packed_a;
+                pa.buf = (uint8_t *)pa.buf + i0 * pa.ld * esz;
+                pa.m = (size_t)len;
+            }
+            if ((r = run_product(rg, in, e, len, k, n, ptr_add(a, i0 * rsa * esz), rsa, csa, bsa,
+                                 b, rsb, csb, bsb, (void *)ptr_add(c, i0 * rsc * osz), rsc, csc,
+                                 bsc, batch, packed, packed_a ? &pa : nullptr)))
+                return r;
+        }
+        return ok();
+    }
+    if (n > kMaxSide) {
+        for (int64_t j0 = 0; j0 < n; j0 += kMaxSide) {
+            const int64_t len = std::min(kMaxSide, n - j0);
+            EpiParams e = ep;
+            channel_shift(e, 1, j0);
+            gk_packed_rhs pb;
+            if (packed) {
+                pb = *packed;
+                pb.buf = (uint8_t *)pb.buf + j0 * pb.ld * esz;
+                pb.n = (size_t)len;
+            }
+            if ((r = run_product(rg, in, e, m, k, len, a, rsa, csa, bsa,
+                                 ptr_add(b, j0 * csb * esz), rsb, csb, bsb,
+                                 (void *)ptr_add(c, j0 * csc * osz), rsc, csc, bsc, batch,
+                                 packed ? &pb : nullptr, packed_a)))
+                return r;
+        }
+        return ok();
+    }
+    const bool gemv_route = std::min(m, n) <= 8;
+    const bool too_long = gemv_route ? k > kGemvMaxK : k * esz > kMaxTileRowBytes;
+    if (!too_long)
+        return run_fit(rg, in, ep, m, k, n, a, rsa, csa, bsa, b, rsb, csb, bsb, c, rsc, csc, bsc,
+                       batch, packed, packed_a);
+
+    // K slices into a native slab (m x n row-major per element), then the
+    // call's epilogue.  The slab and the slices' pack space are taken at once:
+    // a slice's inner call packs both operands (their rows are longer than the
+    // kernels address) into the space behind the slab.
+    const int64_t S = kSliceBytes / esz;
+    const size_t slab = (size_t)round_up64(batch * m * n * 4, 256);
+    const size_t inner = (size_t)(round_up64(batch * m * S * esz, 256) +
+                                  round_up64(batch * n * S * esz, 256) + kSlabMax);
+    uint8_t *base = nullptr;
+    if ((r = region_get(rg, slab + inner, &base))) return r;
+    const Region in_rg{nullptr, base + slab, inner};
+    EpiParams pe{};
+    pe.kind = in == InType::I8 ? EpiKind::I32 : EpiKind::F32;
+    pe.alpha_i = 1;
+    pe.alpha_f = 1.0f;
+    for (int64_t s0 = 0; s0 < k; s0 += S) {
+        const int64_t len = std::min(S, k - s0);
+        pe.beta_i = s0 ? 1 : 0;
+        pe.beta_f = s0 ? 1.0f : 0.0f;
+        gk_packed_rhs pb;
+        gk_packed_lhs pa;
+        if (packed) {
+            pb = *packed;
+            pb.buf = (uint8_t *)pb.buf + s0 * esz;
+            pb.k = (size_t)len;
+        }
+        if (packed_a) {
+            pa = *packed_a;
+            pa.buf = (uint8_t *)pa.buf + s0 * esz;
+            pa.k = (size_t)len;
+        }
+        if ((r = run_fit(in_rg, in, pe, m, len, n, ptr_add(a, s0 * csa * esz), rsa, csa, bsa,
+                         ptr_add(b, s0 * rsb * esz), rsb, csb, bsb, base, n, 1, m * n, batch,
+                         packed ? &pb : nullptr, packed_a ? &pa : nullptr)))
+            return r;
+    }
+    EpiParams fe = ep;
+    fe.c = c;
+    fe.rsc = rsc;
+    fe.csc = csc;
+    fe.bsc = bsc;
+    fe.vec4 = csc == 1 && (m == 1 || rsc % 4 == 0) && (batch <= 1 || bsc % 4 == 0) &&
+              ((uintptr_t)c % (uintptr_t)(4 * osz)) == 0;
+    hipError_t e = launch_split_reduce(in, base, 1, m, n, batch, fe, tl_stream);
+    if (e != hipSuccess) return hip_fail(e, "k-slice epilogue launch");
+    return finish("mfma gemm (K sliced)");
+}
+
+// One launch's worth of product (the limits above hold).
+int run_fit(const Region &rg, InType in, EpiParams ep, int64_t m, int64_t k, int64_t n,
+            const void *a, int64_t rsa, int64_t csa, int64_t bsa, const void *b, int64_t rsb,
+            int64_t csb, int64_t bsb, void *c, int64_t rsc, int64_t csc, int64_t bsc,
+            int64_t batch, const gk_packed_rhs *packed, const gk_packed_lhs *packed_a) {
     const size_t esz = in_size(in);
     // Orientation: the kernels write C row-major-ish (kernel column index the
     // fast one), so a column-major-ish C computes C^T = B^T A^T -- a swap of
@@ -519,48 +742,58 @@ int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t
         ep.csc = csc;
     }
 
-    gk_workspace *ws = resolve_ws(ws_in);
-    const bool a_ok = canonical(A, M, k, esz, batch);
-    const bool b_ok = canonical(Bt, N, k, esz, batch);
-
-    // Route.  The matrix-core kernels address a tile's rows with 32-bit
-    // offsets from its first row: 256 row strides plus a row must stay below
-    // 2 GiB (row strides as they will be after any pack).
-    const int64_t pld = round_up64(std::max<int64_t>(k, 1), 16 / (int64_t)esz);
-    const int64_t a_rs = a_ok ? A.rs : pld, b_rs = b_ok ? Bt.rs : pld;
-    const bool k_fits = k * (int64_t)esz <= kMaxTileRowBytes;
-    const bool offsets_fit = std::max(a_rs, b_rs) * (int64_t)esz <= kMaxTileRowBytes && k_fits;
+    // Route.  The matrix-core and skinny kernels address a tile's rows with
+    // 32-bit offsets from its first row: 256 row strides plus a row must stay
+    // below 2 GiB, so an operand with a longer row stride is packed (to rows
+    // of K, which the caller keeps within that bound).
+    const int64_t kbytes = k * (int64_t)esz;
+    const bool a_ok = canonical(A, M, k, esz, batch) && A.rs * (int64_t)esz <= kMaxTileRowBytes;
+    const bool b_ok = canonical(Bt, N, k, esz, batch) && Bt.rs * (int64_t)esz <= kMaxTileRowBytes;
+    const bool k_fits = kbytes <= kMaxTileRowBytes;
     const int64_t short_side = std::min(M, N);
     // Skinny products: the short side's rows are the vectors.  One vector
     // streams best with the wavefront GEMV (a whole 1 KiB row segment per
     // load, no cross-wave exchange); 2..16 vectors go to the matrix-core
     // skinny kernel, which stages the vectors from any strides itself (only
     // the long operand must be k-contiguous), except the few short sides
-    // gemv_beats_skinny names.
+    // gemv_beats_skinny names.  The choice depends on the shape and element
+    // type only, so a batched element, a problem of a pointer-array batch and
+    // the standalone call take the same kernel (and sum in the same order)
+    // whatever their strides and alignment; the GEMV gets packed operands
+    // when they are not k-contiguous.
     const bool vec_is_a = M <= N;
-    const bool gemv_first = a_ok && b_ok && gemv_beats_skinny(in, short_side, k * (int64_t)esz);
-    const bool skinny_ok = short_side >= 2 && short_side <= 16 && !gemv_first && skinny_enabled() && k_fits &&
-                           (vec_is_a ? b_rs : a_rs) * (int64_t)esz <= kMaxTileRowBytes &&
+    const bool gemv_first = gemv_beats_skinny(in, short_side, kbytes);
+    const bool skinny_ok = short_side >= 2 && short_side <= 16 && !gemv_first &&
+                           skinny_enabled() && k_fits &&
                            skinny_lds_bytes(in, k, (int)short_side) <= kSkinnyLdsMax;
     const bool vector_route = skinny_ok || short_side <= 8;
     const bool pack_a = !a_ok && !(skinny_ok && vec_is_a);
     const bool pack_b = !b_ok && !(skinny_ok && !vec_is_a);
+    // Split K.  Float products split by the element shape only (a batched
+    // element sums in the same order as the standalone product); i8 sums do
+    // not depend on the split (wrapping addition), so an i8 batch that fills
+    // the CUs by itself is not split.
     int splits = vector_route ? 1 : choose_splits(M, N, k, esz);
+    if (splits > 1 && in == InType::I8 && batch > 1 &&
+        choose_splits(M, N * batch, k, esz) == 1)
+        splits = 1;
     // K ranges of whole 64-byte stages; rounding up may leave fewer ranges,
     // every one of them non-empty.
     const int64_t kchunk = splits > 1 ? round_up64((k + splits - 1) / splits, 64 / (int64_t)esz) : k;
     splits = (int)((k + kchunk - 1) / kchunk);
-    const size_t part_bytes =
-        splits > 1 ? (size_t)round_up64((int64_t)batch * splits * M * N * 4, 256) : 0;
+    // Batch elements per split-K launch: as many as kSlabMax of partial sums
+    // holds (at least one).
+    const int64_t elem_part = (int64_t)splits * M * N * 4;
+    const int64_t zchunk = splits > 1 ? std::max<int64_t>(1, std::min(batch, kSlabMax / elem_part)) : batch;
+    const size_t part_bytes = splits > 1 ? (size_t)round_up64(zchunk * elem_part, 256) : 0;
 
     uint8_t *part = nullptr;
     if (pack_a || pack_b || part_bytes) {
         const size_t a_bytes = pack_a ? pack_bytes(in, M, k, batch, A) : 0;
         const size_t b_bytes = pack_b ? pack_bytes(in, N, k, batch, Bt) : 0;
-        void *base = nullptr;
-        int r = ws_reserve(ws, a_bytes + b_bytes + part_bytes, &base);
+        uint8_t *dst = nullptr;
+        int r = region_get(rg, a_bytes + b_bytes + part_bytes, &dst);
         if (r) return r;
-        uint8_t *dst = (uint8_t *)base;
         if (pack_a && (r = materialize(in, A, M, k, batch, dst, &A))) return r;
         if (pack_b && (r = materialize(in, Bt, N, k, batch, dst + a_bytes, &Bt))) return r;
         part = dst + a_bytes + b_bytes;
@@ -570,46 +803,34 @@ int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t
     if (vector_route) {
         // Skinny route: the short side's rows are the vectors, streamed
         // against the long side's rows (matrix-core kernel up to 16 vectors
-        // when the vectors fit in LDS, else the wavefront-reduction GEMV).
+        // when the vectors fit in LDS, else the wavefront-reduction GEMV),
+        // every batch element in one launch (grid y).
         GemvArgs g{};
         EpiParams eg = ep;
+        const Opnd &mat = vec_is_a ? Bt : A;
+        const Opnd &vec = vec_is_a ? A : Bt;
         if (vec_is_a) {
-            g.mat = Bt.p; g.ld = Bt.rs; g.vec = A.p; g.vld = A.rs; g.vks = A.ks;
             g.R = (int32_t)N; g.nvec = (int32_t)M;
         } else {
-            g.mat = A.p; g.ld = A.rs; g.vec = Bt.p; g.vld = Bt.rs; g.vks = Bt.ks;
             g.R = (int32_t)M; g.nvec = (int32_t)N;
             std::swap(eg.rsc, eg.csc);
             eg.axis ^= 1;
         }
+        g.mat = mat.p; g.ld = mat.rs; g.bsm = mat.bs;
+        g.vec = vec.p; g.vld = vec.rs; g.vks = vec.ks; g.bsv = vec.bs;
         g.K = (int32_t)k;
         g.cus = g_num_cus;
-        const Opnd &mat = vec_is_a ? Bt : A;
-        const Opnd &vec = vec_is_a ? A : Bt;
-        const int64_t osz = ep.kind == EpiKind::Q8 ? 1 : (ep.kind == EpiKind::BF16 ? 2 : 4);
-        for (int64_t z = 0; z < batch; ++z) {
-            GemvArgs gz = g;
-            gz.mat = (const uint8_t *)mat.p + z * mat.bs * (int64_t)esz;
-            gz.vec = (const uint8_t *)vec.p + z * vec.bs * (int64_t)esz;
-            EpiParams ez = eg;
-            ez.c = (uint8_t *)ep.c + z * bsc * osz;
-            e = skinny_ok ? launch_skinny(in, gz, ez, tl_stream) : launch_gemv(in, gz, ez, tl_stream);
-            if (e != hipSuccess) return hip_fail(e, skinny_ok ? "skinny launch" : "gemv launch");
-        }
+        g.batch = (int32_t)batch;
+        e = skinny_ok ? launch_skinny(in, g, eg, tl_stream) : launch_gemv(in, g, eg, tl_stream);
+        if (e != hipSuccess) return hip_fail(e, skinny_ok ? "skinny launch" : "gemv launch");
         return finish(skinny_ok ? "skinny" : "gemv");
     }
 
     // Whole 4-element output chunks can go out as one vector access when C is
     // unit-stride along the kernel's columns and every chunk start is aligned.
-    {
-        const int64_t osz = ep.kind == EpiKind::Q8 ? 1 : (ep.kind == EpiKind::BF16 ? 2 : 4);
-        ep.vec4 = ep.csc == 1 && (M == 1 || ep.rsc % 4 == 0) && (batch <= 1 || bsc % 4 == 0) &&
-                  ((uintptr_t)c % (uintptr_t)(4 * osz)) == 0;
-    }
-    if (!offsets_fit)
-        return fail(GK_ERR_OVERFLOW,
-                    "gemmkit: rows too long for the device kernels (K or a row stride above "
-                    "%lld elements)", (long long)(kMaxTileRowBytes / (int64_t)esz));
+    const int64_t osz = out_size(ep.kind);
+    ep.vec4 = ep.csc == 1 && (M == 1 || ep.rsc % 4 == 0) && (batch <= 1 || bsc % 4 == 0) &&
+              ((uintptr_t)c % (uintptr_t)(4 * osz)) == 0;
     MmaArgs args{};
     args.a = A.p;
     args.b = Bt.p;
@@ -625,7 +846,7 @@ int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t
     if (splits > 1) {
         // Partial sums of each K range into their own slab (i32 for i8
         // inputs, f32 otherwise), then one pass sums the slabs in range order
-        // and applies the call's epilogue.
+        // and applies the call's epilogue; zchunk batch elements at a time.
         args.splits = splits;
         args.kchunk = (int32_t)kchunk;
         EpiParams pe{};
@@ -637,13 +858,20 @@ int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t
         pe.csc = 1;
         pe.bsc = M * N;
         pe.vec4 = N % 4 == 0;
-        e = launch_mma(in, Tile::T64x64, args, pe, tl_stream);
-        if (e != hipSuccess) return hip_fail(e, "mfma launch");
-        e = launch_split_reduce(in, part, splits, M, N, batch, ep, tl_stream);
-        if (e != hipSuccess) return hip_fail(e, "split reduce launch");
+        for (int64_t z0 = 0; z0 < batch; z0 += zchunk) {
+            MmaArgs az = args;
+            az.batch = (int32_t)std::min(zchunk, batch - z0);
+            az.a = ptr_add(A.p, z0 * A.bs * (int64_t)esz);
+            az.b = ptr_add(Bt.p, z0 * Bt.bs * (int64_t)esz);
+            EpiParams ez = ep;
+            ez.c = (void *)ptr_add(ep.c, z0 * bsc * osz);
+            e = launch_mma(in, Tile::T64x64, az, pe, tl_stream);
+            if (e != hipSuccess) return hip_fail(e, "mfma launch");
+            e = launch_split_reduce(in, part, splits, M, N, az.batch, ez, tl_stream);
+            if (e != hipSuccess) return hip_fail(e, "split reduce launch");
+        }
         return finish("mfma gemm (split K)");
     }
-    const int64_t kbytes = k * (int64_t)esz;
     double cost_whole = 0.0;
     const Tile tile = pick_tile(M, N, batch, kbytes, ep.kind, in, &cost_whole);
     bool forced;
@@ -659,14 +887,8 @@ int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t
         a2.N = (int32_t)(N - ts.na);
         a2.b = (const uint8_t *)Bt.p + ts.na * Bt.rs * (int64_t)esz;
         EpiParams e2 = ep;
-        const int64_t osz = ep.kind == EpiKind::Q8 ? 1 : (ep.kind == EpiKind::BF16 ? 2 : 4);
         e2.c = (uint8_t *)ep.c + ts.na * ep.csc * osz;
-        if (ep.axis == 1) {
-            if (e2.scales) e2.scales += ts.na;
-            if (e2.bias) e2.bias += ts.na;
-            if (e2.fbias)
-                e2.fbias = (const uint8_t *)e2.fbias + ts.na * (ep.kind == EpiKind::BF16 ? 2 : 4);
-        }
+        channel_shift(e2, 1, ts.na);
         e = launch_mma(in, ts.ta, a1, ep, tl_stream);
         if (e != hipSuccess) return hip_fail(e, "mfma launch");
         e = launch_mma(in, ts.tb, a2, e2, tl_stream);
@@ -678,9 +900,27 @@ int run_product(gk_workspace *ws_in, InType in, EpiParams ep, int64_t m, int64_t
     return finish("mfma gemm");
 }
 
+// Sizes the reference accepts (it fails closed only where its pack sizes
+// overflow, src/workspace.rs:25-45): every dimension and element count must be
+// addressable with signed 64-bit element offsets.
 bool dims_fit(size_t m, size_t k, size_t n, size_t batch) {
-    const size_t lim = (size_t)INT32_MAX;
-    return m <= lim && k <= lim && n <= lim && batch <= 65535;
+    const size_t lim = (size_t)INT64_MAX / 16;
+    return m <= lim && k <= lim && n <= lim && batch <= lim;
+}
+
+// Calls fn(z0, nb, i0, mm, j0, nn) over blocks of a (batch x) m x n user-frame
+// C of at most kMaxGridZ elements, kMaxSide rows and kMaxSide columns (the
+// element-wise fill kernels index one block per launch).
+template <typename F>
+hipError_t for_c_blocks(int64_t m, int64_t n, int64_t batch, F fn) {
+    for (int64_t z0 = 0; z0 < batch; z0 += kMaxGridZ)
+        for (int64_t i0 = 0; i0 < m; i0 += kMaxSide)
+            for (int64_t j0 = 0; j0 < n; j0 += kMaxSide) {
+                hipError_t e = fn(z0, std::min(kMaxGridZ, batch - z0), i0,
+                                  std::min(kMaxSide, m - i0), j0, std::min(kMaxSide, n - j0));
+                if (e != hipSuccess) return e;
+            }
+    return hipSuccess;
 }
 
 // Degenerate C <- beta*C (k == 0 or alpha == 0).
@@ -688,10 +928,41 @@ int scale_c(EpiKind kind, void *c, size_t m, size_t n, ptrdiff_t rsc, ptrdiff_t 
             size_t batch, ptrdiff_t bsc, int32_t beta_i, float beta_f) {
     bool one = (kind == EpiKind::I32) ? beta_i == 1 : beta_f == 1.0f;
     if (one) return ok();
-    hipError_t e = launch_scale_c(kind, c, (int64_t)m, (int64_t)n, rsc, csc, (int64_t)batch, bsc,
-                                  beta_i, beta_f, tl_stream);
+    const int64_t osz = out_size(kind);
+    hipError_t e = for_c_blocks((int64_t)m, (int64_t)n, (int64_t)batch,
+                                [&](int64_t z0, int64_t nb, int64_t i0, int64_t mm, int64_t j0,
+                                    int64_t nn) {
+        void *cb = (void *)ptr_add(c, (z0 * bsc + i0 * rsc + j0 * csc) * osz);
+        return launch_scale_c(kind, cb, mm, nn, rsc, csc, nb, bsc, beta_i, beta_f, tl_stream);
+    });
     if (e != hipSuccess) return hip_fail(e, "scale_c launch");
     return finish("scale_c");
+}
+
+// The fused degenerate map over a (batch x) m x n user-frame C (`ep` in the
+// user frame).
+hipError_t fused_fill_blocks(const EpiParams &ep, int64_t m, int64_t n, int64_t batch) {
+    const int64_t osz = out_size(ep.kind);
+    return for_c_blocks(m, n, batch, [&](int64_t z0, int64_t nb, int64_t i0, int64_t mm,
+                                         int64_t j0, int64_t nn) {
+        EpiParams e = ep;
+        e.c = (void *)ptr_add(ep.c, (z0 * ep.bsc + i0 * ep.rsc + j0 * ep.csc) * osz);
+        channel_shift(e, 0, i0);
+        channel_shift(e, 1, j0);
+        return launch_fused_fill(e, mm, nn, nb, tl_stream);
+    });
+}
+
+// The k == 0 requant fill over an m x n user-frame C.
+hipError_t requant_fill_blocks(const EpiParams &ep, int64_t m, int64_t n) {
+    return for_c_blocks(m, n, 1, [&](int64_t, int64_t, int64_t i0, int64_t mm, int64_t j0,
+                                     int64_t nn) {
+        EpiParams e = ep;
+        e.c = (void *)ptr_add(ep.c, i0 * ep.rsc + j0 * ep.csc);
+        channel_shift(e, 0, i0);
+        channel_shift(e, 1, j0);
+        return launch_requant_fill(e, mm, nn, tl_stream);
+    });
 }
 
 EpiParams epi_int(int32_t alpha, int32_t beta) {
@@ -721,13 +992,14 @@ float bf16_to_f32(gk_bf16 h) {
 int exec_i8(gk_workspace *ws, size_t m, size_t k, size_t n, int32_t alpha, const int8_t *a,
             ptrdiff_t rsa, ptrdiff_t csa, const int8_t *b, ptrdiff_t rsb, ptrdiff_t csb,
             int32_t beta, int32_t *c, ptrdiff_t rsc, ptrdiff_t csc,
-            const gk_packed_rhs *packed = nullptr) {
+            const gk_packed_rhs *packed = nullptr, const Region *fixed = nullptr) {
     int r;
     if ((r = device_init())) return r;
     if (m == 0 || n == 0) return ok();
-    if (!dims_fit(m, k, n, 1)) return fail(GK_ERR_OVERFLOW, "gemmkit: dimensions exceed 2^31-1");
+    if (!dims_fit(m, k, n, 1)) return fail(GK_ERR_OVERFLOW, "gemmkit: GEMM is too large; the pack workspace size overflows usize");
     if (k == 0 || alpha == 0) return scale_c(EpiKind::I32, c, m, n, rsc, csc, 1, 0, beta, 0.f);
-    return run_product(ws, InType::I8, epi_int(alpha, beta), m, k, n, a, rsa, csa, 0, b, rsb, csb,
+    return run_product(fixed ? *fixed : Region{ws, nullptr, 0}, InType::I8, epi_int(alpha, beta),
+                       m, k, n, a, rsa, csa, 0, b, rsb, csb,
                        0, c, rsc, csc, 0, 1, packed);
 }
 
@@ -763,7 +1035,7 @@ int exec_float(gk_workspace *ws, InType in, EpiKind kind, size_t batch, size_t m
     if ((r = device_init())) return r;
     if (fx && (r = check_fused_enums(*fx))) return r;
     if (batch == 0 || m == 0 || n == 0) return ok();
-    if (!dims_fit(m, k, n, batch)) return fail(GK_ERR_OVERFLOW, "gemmkit: dimensions exceed 2^31-1");
+    if (!dims_fit(m, k, n, batch)) return fail(GK_ERR_OVERFLOW, "gemmkit: GEMM is too large; the pack workspace size overflows usize");
     EpiParams ep = epi_float(kind, alpha, beta);
     if (fx) {
         ep.fbias = fx->bias;
@@ -778,11 +1050,12 @@ int exec_float(gk_workspace *ws, InType in, EpiKind kind, size_t batch, size_t m
         ep.rsc = rsc;
         ep.csc = csc;
         ep.bsc = bsc;
-        hipError_t e = launch_fused_fill(ep, (int64_t)m, (int64_t)n, (int64_t)batch, tl_stream);
+        hipError_t e = fused_fill_blocks(ep, (int64_t)m, (int64_t)n, (int64_t)batch);
         if (e != hipSuccess) return hip_fail(e, "fused fill launch");
         return finish("fused fill");
     }
-    return run_product(ws, in, ep, m, k, n, a, rsa, csa, bsa, b, rsb, csb, bsb, c, rsc, csc, bsc,
+    return run_product(Region{ws, nullptr, 0}, in, ep, m, k, n, a, rsa, csa, bsa, b, rsb, csb, bsb,
+                       c, rsc, csc, bsc,
                        batch, packed, packed_a);
 }
 
@@ -799,7 +1072,7 @@ int exec_requant(gk_workspace *ws, size_t m, size_t k, size_t n, const int8_t *a
     if (act != GK_ACT_NONE && act != GK_ACT_RELU)
         return fail(GK_ERR_ARG, "gemmkit: requantize act (%d) must be 0 (none) or 1 (relu)", act);
     if (m == 0 || n == 0) return ok();
-    if (!dims_fit(m, k, n, 1)) return fail(GK_ERR_OVERFLOW, "gemmkit: dimensions exceed 2^31-1");
+    if (!dims_fit(m, k, n, 1)) return fail(GK_ERR_OVERFLOW, "gemmkit: GEMM is too large; the pack workspace size overflows usize");
     EpiParams ep{};
     ep.kind = EpiKind::Q8;
     ep.scale = scale;
@@ -813,11 +1086,12 @@ int exec_requant(gk_workspace *ws, size_t m, size_t k, size_t n, const int8_t *a
         ep.c = c;
         ep.rsc = rsc;
         ep.csc = csc;
-        hipError_t e = launch_requant_fill(ep, (int64_t)m, (int64_t)n, tl_stream);
+        hipError_t e = requant_fill_blocks(ep, (int64_t)m, (int64_t)n);
         if (e != hipSuccess) return hip_fail(e, "requant fill launch");
         return finish("requant fill");
     }
-    return run_product(ws, InType::I8, ep, m, k, n, a, rsa, csa, 0, b, rsb, csb, 0, c, rsc, csc,
+    return run_product(Region{ws, nullptr, 0}, InType::I8, ep, m, k, n, a, rsa, csa, 0, b, rsb,
+                       csb, 0, c, rsc, csc,
                        0, 1, packed);
 }
 
@@ -1307,7 +1581,7 @@ int run_problems(gk_workspace *ws, InType in, const P *problems, size_t count, S
                        elem_step(p.b, q.b, esz, &qb) && qb == sb * (ptrdiff_t)(idx - i) &&
                        elem_step(p.c, q.c, esz, &qc) && qc == sc * (ptrdiff_t)(idx - i);
             };
-            while (j < count && j - i < 65535 && same(problems[j], j)) ++j;
+            while (j < count && same(problems[j], j)) ++j;
         }
         int r;
         if (j - i > 1)
@@ -1413,6 +1687,18 @@ int gk_set_synchronous(int on) {
 }
 
 gk_workspace *gk_workspace_new(void) { return new gk_workspace(); }
+
+gk_workspace *gk_workspace_with_capacity(size_t bytes) {
+    gk_workspace *ws = new gk_workspace();
+    if (bytes > 0) {
+        void *p = nullptr;
+        if (device_init() || ws_reserve(ws, bytes, &p)) {
+            delete ws;
+            return nullptr;
+        }
+    }
+    return ws;
+}
 
 void gk_workspace_free(gk_workspace *ws) {
     if (!ws) return;

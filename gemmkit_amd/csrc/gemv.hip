@@ -118,7 +118,7 @@ __device__ __forceinline__ void store_group(const GemvArgs &g, const EpiParams &
     if ((lane & ((1 << SH) - 1)) == 0) {
         const int idx = lane >> SH;
         const int r = idx / NV, j = idx % NV;
-        if (j < g.nvec && r0 + r < g.R) Store<E>::apply(ep, 0, j, (int)(r0 + r), v[0]);
+        if (j < g.nvec && r0 + r < g.R) Store<E>::apply(ep, blockIdx.y, j, (int)(r0 + r), v[0]);
     }
 }
 
@@ -131,8 +131,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_reg(const GemvArgs g, const
     // the pack, which zero-fills both operands' rows up to the next 16 bytes.
     const int nch = (int)(((int64_t)g.K * esz + 15) / 16);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint8_t *mat = (const uint8_t *)g.mat;
-    const uint8_t *vec = (const uint8_t *)g.vec;
+    const int64_t zb = blockIdx.y;  // batch element
+    const uint8_t *mat = (const uint8_t *)g.mat + zb * g.bsm * esz;
+    const uint8_t *vec = (const uint8_t *)g.vec + zb * g.bsv * esz;
     const int64_t ld_b = g.ld * esz, vld_b = g.vld * esz;
 
     v4i_g x[NV][CPL];
@@ -199,7 +200,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_lds(const GemvArgs g, const
     constexpr int esz = (T == InType::I8) ? 1 : (T == InType::BF16 ? 2 : 4);
     const int64_t nch = ((int64_t)g.K * esz + 15) / 16;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint8_t *vec = (const uint8_t *)g.vec;
+    const int64_t zb = blockIdx.y;  // batch element
+    const uint8_t *vec = (const uint8_t *)g.vec + zb * g.bsv * esz;
     const int64_t vld_b = g.vld * esz;
     // Vectors beyond nvec (up to NV) read as zeros; when the block does not
     // fit in LDS the vectors are read from global memory (L2-resident).
@@ -216,7 +218,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_lds(const GemvArgs g, const
         if (staged) return *(const v4i_g *)(sv + (j * nch + ch) * 16);
         return j < g.nvec ? *(const v4i_g *)(vec + j * vld_b + ch * 16) : v4i_g{0, 0, 0, 0};
     };
-    const uint8_t *mat = (const uint8_t *)g.mat;
+    const uint8_t *mat = (const uint8_t *)g.mat + zb * g.bsm * esz;
     const int64_t ld_b = g.ld * esz;
     const int64_t groups = ((int64_t)g.R + RPW - 1) / RPW;
     const int64_t stride = (int64_t)gridDim.x * kGemvWaves;
@@ -267,12 +269,14 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_lds(const GemvArgs g, const
 }
 
 // Persistent grid: enough workgroups to cover the row groups, at most
-// `per_cu` per CU.
-static unsigned gemv_grid(int64_t groups, int cus, int per_cu) {
+// `per_cu` per CU over all batch elements (grid y); every element gets at
+// least one workgroup.
+static dim3 gemv_grid(int64_t groups, int cus, int per_cu, int batch) {
     int64_t blocks = (groups + kGemvWaves - 1) / kGemvWaves;
-    const int64_t cap = (int64_t)(cus > 0 ? cus : 256) * per_cu;
+    const int64_t nb = batch > 1 ? batch : 1;
+    const int64_t cap = ((int64_t)(cus > 0 ? cus : 256) * per_cu + nb - 1) / nb;
     if (blocks > cap) blocks = cap;
-    return (unsigned)(blocks < 1 ? 1 : blocks);
+    return dim3((unsigned)(blocks < 1 ? 1 : blocks), (unsigned)nb);
 }
 
 // Rows per wave iteration and workgroups per CU, from a graph-timed sweep over
@@ -297,7 +301,7 @@ template <InType T, EpiKind E, int NV, int CPL>
 static hipError_t go_reg(const GemvArgs &g, const EpiParams &ep, hipStream_t stream) {
     constexpr int RPW = rows_per_wave<CPL>();
     const int64_t groups = ((int64_t)g.R + RPW - 1) / RPW;
-    hipLaunchKernelGGL((gemv_reg<T, E, NV, CPL, RPW>), dim3(gemv_grid(groups, g.cus, reg_per_cu<CPL>())),
+    hipLaunchKernelGGL((gemv_reg<T, E, NV, CPL, RPW>), gemv_grid(groups, g.cus, reg_per_cu<CPL>(), g.batch),
                        dim3(kGemvThreads), 0, stream, g, ep);
     return hipGetLastError();
 }
@@ -309,7 +313,7 @@ static hipError_t go_lds(const GemvArgs &g, const EpiParams &ep, hipStream_t str
     const int64_t vbytes = (int64_t)NV * (((int64_t)g.K * esz + 15) / 16) * 16;
     const size_t shm = vbytes <= kGemvLdsMax ? (size_t)vbytes : 0;
     const int64_t groups = ((int64_t)g.R + RPW - 1) / RPW;
-    hipLaunchKernelGGL((gemv_lds<T, E, NV, RPW>), dim3(gemv_grid(groups, g.cus, 2)),
+    hipLaunchKernelGGL((gemv_lds<T, E, NV, RPW>), gemv_grid(groups, g.cus, 2, g.batch),
                        dim3(kGemvThreads), shm, stream, g, ep);
     return hipGetLastError();
 }
@@ -343,7 +347,10 @@ static hipError_t gemv_nv(const GemvArgs &g, const EpiParams &ep, hipStream_t st
 }
 
 hipError_t launch_gemv(InType in, const GemvArgs &g, const EpiParams &ep, hipStream_t stream) {
-    if (g.nvec < 1 || g.nvec > 8 || g.R < 1) return hipErrorInvalidValue;
+    // Row addresses are formed in 64 bits (any non-negative row stride); the
+    // host packs a matrix with a negative one.
+    if (g.nvec < 1 || g.nvec > 8 || g.R < 1 || g.ld < 0 || g.batch < 1 || g.batch > kMaxGridZ)
+        return hipErrorInvalidValue;
     switch (in) {
     case InType::I8:
         if (ep.kind == EpiKind::I32) return gemv_nv<InType::I8, EpiKind::I32>(g, ep, stream);

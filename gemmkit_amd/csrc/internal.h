@@ -93,9 +93,17 @@ struct GemvArgs {
     int64_t vld, vks;      // vks == 1 (k-contiguous) except on the skinny route
     int32_t R, K, nvec;
     int32_t cus;           // compute units of the device (persistent grid size)
-    // Output element (vector j, matrix row r) is stored as the epilogue's
-    // (row j, column r): at c + j*rsc + r*csc of the EpiParams.
+    int32_t batch;         // batch elements (grid y), at most kMaxGridZ
+    int64_t bsm, bsv;      // batch strides of mat and vec in elements
+    // Output element (vector j, matrix row r) of batch element z is stored as
+    // the epilogue's (row j, column r) of element z: at c + z*bsc + j*rsc +
+    // r*csc of the EpiParams.  Each element's arithmetic does not depend on
+    // the batch count or the grid size.
 };
+
+// Batch elements one launch covers (grid z of the tiles, grid y of the
+// skinny and GEMV kernels).
+constexpr int64_t kMaxGridZ = 65535;
 hipError_t launch_gemv(InType in, const GemvArgs &g, const EpiParams &ep, hipStream_t stream);
 
 // Matrix-core skinny route (1..16 vectors): the vectors are staged in LDS,

@@ -6,6 +6,9 @@ namespace gk {
 
 hipError_t launch_mma(InType in, Tile tile, const MmaArgs &args, const EpiParams &ep,
                       hipStream_t stream) {
+    // Tile rows are addressed as unsigned 32-bit offsets from the tile's
+    // first row: row strides must be non-negative (the host packs otherwise).
+    if (args.lda < 0 || args.ldb < 0) return hipErrorInvalidValue;
     switch (in) {
     case InType::I8: return launch_mma_i8(tile, args, ep, stream);
     case InType::BF16: return launch_mma_bf16(tile, args, ep, stream);

@@ -133,9 +133,11 @@ __global__ __launch_bounds__(kSkThreads) void skinny_mfma(const GemvArgs g, cons
     // item boundaries too.  (Issuing batch 1 before the vector staging as
     // well measured slower: 14.3 against 12.6 us on the 14336x4096 i8
     // weight with 8 vectors.)
-    const uint8_t *mat = (const uint8_t *)g.mat;
+    const int64_t zb = blockIdx.y;  // batch element
+    const uint8_t *mat = (const uint8_t *)g.mat + zb * g.bsm * esz;
     const int64_t ld_b = g.ld * esz;
-    const int items = (g.R + kSkRows - 1) / kSkRows;
+    // (64-bit: R may be up to 2^31 - 1; every item's first row is below R)
+    const int items = (int)(((int64_t)g.R + kSkRows - 1) / kSkRows);
     const int my_items = (int)blockIdx.x < items ? (items - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
     const int nbw = ks1 > ks0 ? (ks1 - ks0 + kSkPF - 1) / kSkPF : 1;
     const int total = my_items * nbw;
@@ -166,7 +168,7 @@ __global__ __launch_bounds__(kSkThreads) void skinny_mfma(const GemvArgs g, cons
     // Stage the vectors: nvec rows of kb bytes (zeros past K), 8 chunks or
     // elements per thread in flight at a time (one L2 round trip for up to
     // 32 KiB).
-    const uint8_t *vec = (const uint8_t *)g.vec;
+    const uint8_t *vec = (const uint8_t *)g.vec + zb * g.bsv * esz;
     const int64_t vld_b = g.vld * esz;
     if (g.vks == 1 && g.K * esz % 16 == 0 && vld_b % 16 == 0 && (uintptr_t)vec % 16 == 0) {
         const int64_t cpr = kb / 16, nchunks = nvec * cpr;
@@ -289,8 +291,9 @@ __global__ __launch_bounds__(kSkThreads) void skinny_mfma(const GemvArgs g, cons
             val_t sum = comb[x];
 #pragma unroll
             for (int w = 1; w < kSkWaves; ++w) sum += comb[w * BLK * 2 * 64 + x];
-            const int row = r0 + 8 * b + 2 * (ln >> 4) + e, j = ln & 15;
-            if (j < nvec && row < g.R) Store<E>::apply(ep, 0, j, row, sum);
+            const int64_t row = (int64_t)r0 + 8 * b + 2 * (ln >> 4) + e;
+            const int j = ln & 15;
+            if (j < nvec && row < g.R) Store<E>::apply(ep, zb, j, (int)row, sum);
         }
         __syncthreads();
     };
@@ -316,24 +319,33 @@ static hipError_t skinny_go(const GemvArgs &g, const EpiParams &ep, hipStream_t 
     const int cus = g.cus > 0 ? g.cus : 256;
     // 32-row items when there are enough of them for every CU, else 8-row
     // items (4x as many workgroups streaming the same bytes).
-    const bool wide = (g.R + 31) / 32 >= cus;
-    const int64_t items = wide ? (g.R + 31) / 32 : (g.R + 7) / 8;
+    const int64_t R = g.R;
+    const bool wide = (R + 31) / 32 >= cus;
+    const int64_t items = wide ? (R + 31) / 32 : (R + 7) / 8;
     // As many resident workgroups per CU as its 160 KiB of LDS holds (<= 4).
     const int fit = (int)(160 * 1024 / shm);
     const int per_cu = fit < 4 ? (fit > 1 ? fit : 1) : 4;
-    int64_t blocks = (int64_t)cus * per_cu;
+    // Batch elements share the persistent grid (grid y), each at least one
+    // workgroup.
+    const int64_t nb = g.batch > 1 ? g.batch : 1;
+    int64_t blocks = ((int64_t)cus * per_cu + nb - 1) / nb;
     if (blocks > items) blocks = items;
+    const dim3 grid((unsigned)blocks, (unsigned)nb);
     if (wide)
-        hipLaunchKernelGGL((skinny_mfma<T, E, 4>), dim3((unsigned)blocks), dim3(kSkThreads),
-                           (size_t)shm, stream, g, ep);
+        hipLaunchKernelGGL((skinny_mfma<T, E, 4>), grid, dim3(kSkThreads), (size_t)shm, stream, g,
+                           ep);
     else
-        hipLaunchKernelGGL((skinny_mfma<T, E, 1>), dim3((unsigned)blocks), dim3(kSkThreads),
-                           (size_t)shm, stream, g, ep);
+        hipLaunchKernelGGL((skinny_mfma<T, E, 1>), grid, dim3(kSkThreads), (size_t)shm, stream, g,
+                           ep);
     return hipGetLastError();
 }
 
 hipError_t launch_skinny(InType in, const GemvArgs &g, const EpiParams &ep, hipStream_t stream) {
-    if (g.nvec < 1 || g.nvec > 16 || g.R < 1 || skinny_lds_bytes(in, g.K, g.nvec) > kSkinnyLdsMax)
+    // The matrix rows are addressed as unsigned 32-bit offsets from an item's
+    // first row, so its row stride must be non-negative (the vectors may
+    // have any strides).
+    if (g.nvec < 1 || g.nvec > 16 || g.R < 1 || g.ld < 0 || g.batch < 1 || g.batch > kMaxGridZ ||
+        skinny_lds_bytes(in, g.K, g.nvec) > kSkinnyLdsMax)
         return hipErrorInvalidValue;
     switch (in) {
     case InType::I8:

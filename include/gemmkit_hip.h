@@ -87,9 +87,17 @@ void *gk_get_stream(void);
 int gk_set_synchronous(int on);
 
 /* Device scratch arena (src/workspace.rs:53): holds packed operands for
- * layouts the kernels cannot read in place.  Grows on demand, never shrinks. */
+ * layouts the kernels cannot read in place and split-K partial sums.  Grows on
+ * demand (synchronizing the device), never shrinks.  A call made while the
+ * launch stream is being captured into a HIP graph cannot grow it: such a call
+ * fails with GK_ERR_NOMEM when it needs more than the arena holds, so size the
+ * arena before capturing.  The NULL (per-thread) workspace is released when its
+ * worker thread exits. */
 typedef struct gk_workspace gk_workspace;
 gk_workspace *gk_workspace_new(void);
+/* Workspace::with_capacity (src/workspace.rs:78): an arena of at least `bytes`
+ * allocated now; NULL when the device allocation fails. */
+gk_workspace *gk_workspace_with_capacity(size_t bytes);
 void gk_workspace_free(gk_workspace *ws);
 size_t gk_workspace_bytes(const gk_workspace *ws);
 
