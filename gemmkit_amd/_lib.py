@@ -105,6 +105,9 @@ SIGNATURES: dict[str, tuple] = {
     "gk_gemm_i8": (C.c_int, [_vp, _i32, _REF, _REF, _i32, _MUT, _u32]),
     "gk_gemm_i8_unchecked": (C.c_int, [_vp, _size, _size, _size, _i32, _vp, _sdiff, _sdiff,
                                        _vp, _sdiff, _sdiff, _i32, _vp, _sdiff, _sdiff, _u32]),
+    "gk_gemm_i8_unchecked_noalloc": (C.c_int, [_size, _size, _size, _i32, _vp, _sdiff, _sdiff,
+                                               _vp, _sdiff, _sdiff, _i32, _vp, _sdiff, _sdiff,
+                                               _u32]),
     "gk_gemm_i8_requant": (C.c_int, [_vp, _REF, _REF, _REQ, _MUT, _u32]),
     "gk_gemm_i8_requant_u8": (C.c_int, [_vp, _REF, _REF, _REQ, _MUT, _u32]),
     "gk_gemm_i8_requant_unchecked": (C.c_int, [_vp, _size, _size, _size, _vp, _sdiff, _sdiff,

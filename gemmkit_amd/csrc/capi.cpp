@@ -61,6 +61,40 @@ int g_init_status = GK_OK;
 std::string g_init_error;
 int g_num_cus = 256;
 
+// ---------------------------------------------------- no-allocation scratch
+
+// Device scratch of gk_gemm_i8_unchecked_noalloc: packed operands and split-K
+// partial sums of calls that must not allocate.  Each device holds its own
+// copy from module load to process exit.  In host code `scratch` names a
+// host-side stand-in, not device memory: kernels get the per-device address
+// that hipGetSymbolAddress returns (g_scratch_dev), never the array's name.
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t *g_scratch_dev[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up once per device with
+// that device current.
+int scratch_for_current_device(uint8_t **out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(GK_ERR_DEVICE, "gemmkit: device %d is beyond the %d devices the no-allocation "
+                                   "scratch tracks", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        g_scratch_dev[dev] = (uint8_t *)p;
+    }
+    *out = g_scratch_dev[dev];
+    return GK_OK;
+}
+
 int device_init() {
     std::call_once(g_init_once, [] {
         int n = 0;
@@ -76,6 +110,13 @@ int device_init() {
         hipDeviceProp_t prop;
         if (hipGetDeviceProperties(&prop, dev) == hipSuccess && prop.multiProcessorCount > 0)
             g_num_cus = prop.multiProcessorCount;
+        // Set-up of the no-allocation scratch for the initial device (other
+        // devices look theirs up on first use); a failure here surfaces in
+        // the entry point that needs it.
+        uint8_t *sp = nullptr;
+        std::string keep = tl_error;
+        (void)scratch_for_current_device(&sp);
+        tl_error = keep;
     });
     if (g_init_status != GK_OK) return fail(g_init_status, "%s", g_init_error.c_str());
     return GK_OK;
@@ -779,8 +820,25 @@ int run_fit(const Region &rg, InType in, EpiParams ep, int64_t m, int64_t k, int
         splits = 1;
     // K ranges of whole 64-byte stages; rounding up may leave fewer ranges,
     // every one of them non-empty.
+    if (splits > 1) {
+        const int64_t kc = round_up64((k + splits - 1) / splits, 64 / (int64_t)esz);
+        splits = (int)((k + kc - 1) / kc);
+    }
+    const size_t a_bytes = pack_a ? pack_bytes(in, M, k, batch, A) : 0;
+    const size_t b_bytes = pack_b ? pack_bytes(in, N, k, batch, Bt) : 0;
+    // In a fixed scratch region an i8 product takes fewer K ranges when the
+    // partial sums would not fit beside the packed operands (its bits do not
+    // depend on the split).
+    if (rg.fixed && in == InType::I8 && splits > 1) {
+        const int64_t avail = (int64_t)rg.fixed_bytes - (int64_t)(a_bytes + b_bytes);
+        const int64_t fit = avail > 0 ? (avail & ~(int64_t)255) / (M * N * 4) : 0;
+        if (fit < splits) {
+            splits = fit >= 2 ? (int)fit : 1;
+            const int64_t kc = round_up64((k + splits - 1) / splits, 64 / (int64_t)esz);
+            splits = (int)((k + kc - 1) / kc);
+        }
+    }
     const int64_t kchunk = splits > 1 ? round_up64((k + splits - 1) / splits, 64 / (int64_t)esz) : k;
-    splits = (int)((k + kchunk - 1) / kchunk);
     // Batch elements per split-K launch: as many as kSlabMax of partial sums
     // holds (at least one).
     const int64_t elem_part = (int64_t)splits * M * N * 4;
@@ -789,8 +847,6 @@ int run_fit(const Region &rg, InType in, EpiParams ep, int64_t m, int64_t k, int
 
     uint8_t *part = nullptr;
     if (pack_a || pack_b || part_bytes) {
-        const size_t a_bytes = pack_a ? pack_bytes(in, M, k, batch, A) : 0;
-        const size_t b_bytes = pack_b ? pack_bytes(in, N, k, batch, Bt) : 0;
         uint8_t *dst = nullptr;
         int r = region_get(rg, a_bytes + b_bytes + part_bytes, &dst);
         if (r) return r;
@@ -1774,6 +1830,22 @@ int gk_gemm_i8_unchecked(gk_workspace *ws, size_t m, size_t k, size_t n, int32_t
                          ptrdiff_t rsb, ptrdiff_t csb, int32_t beta, int32_t *c, ptrdiff_t rsc,
                          ptrdiff_t csc, gk_par) {
     return exec_i8(ws, m, k, n, alpha, a, rsa, csa, b, rsb, csb, beta, c, rsc, csc);
+}
+
+// The no-allocation twin of gk_gemm_i8_unchecked: the same route and kernels,
+// with the static per-device scratch in place of the workspace arena.  Calls
+// that overlap on one device share that scratch and race.
+int gk_gemm_i8_unchecked_noalloc(size_t m, size_t k, size_t n, int32_t alpha, const int8_t *a,
+                                 ptrdiff_t rsa, ptrdiff_t csa, const int8_t *b, ptrdiff_t rsb,
+                                 ptrdiff_t csb, int32_t beta, int32_t *c, ptrdiff_t rsc,
+                                 ptrdiff_t csc, gk_par) {
+    int r;
+    if ((r = device_init())) return r;
+    uint8_t *sp = nullptr;
+    if ((r = scratch_for_current_device(&sp))) return r;
+    const Region rg{nullptr, sp, kNoAllocScratchBytes};
+    return exec_i8(nullptr, m, k, n, alpha, a, rsa, csa, b, rsb, csb, beta, c, rsc, csc, nullptr,
+                   &rg);
 }
 
 int gk_gemm_i8(gk_workspace *ws, int32_t alpha, const gk_mat_ref *a, const gk_mat_ref *b,

@@ -173,6 +173,21 @@ int gk_gemm_i8_unchecked(gk_workspace *ws, size_t m, size_t k, size_t n, int32_t
                          const int8_t *b, ptrdiff_t rsb, ptrdiff_t csb,
                          int32_t beta, int32_t *c, ptrdiff_t rsc, ptrdiff_t csc, gk_par par);
 
+/* No counterpart in the reference: gk_gemm_i8_unchecked for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments (no workspace), same
+ * kernels and bit-identical results; packed operands and split-K partial sums
+ * go to a static scratch of 64 MiB per device, held from module load to
+ * process exit, instead of a workspace.  It calls no allocator.  A product
+ * that needs more scratch than that fails with GK_ERR_NOMEM before launching
+ * anything.  Every call on a device shares that device's scratch, so calls
+ * that overlap on one device (other threads, other streams) race. */
+int gk_gemm_i8_unchecked_noalloc(size_t m, size_t k, size_t n, int32_t alpha,
+                                 const int8_t *a, ptrdiff_t rsa, ptrdiff_t csa,
+                                 const int8_t *b, ptrdiff_t rsb, ptrdiff_t csb,
+                                 int32_t beta, int32_t *c, ptrdiff_t rsc, ptrdiff_t csc,
+                                 gk_par par);
+
 /* --------------------------------------------------------- requantization */
 
 /* Channel axis of a requant scale vector / bias.  GK_AXIS_ROW is the
