@@ -8,31 +8,37 @@ xorshift* stream, resident in HBM before timing.  A "step" is one gemm_i8 call
 through the C ABI.  The timed region replays a HIP graph holding the K calls
 (captured from the same C-ABI calls on the launch stream), so host-side call
 overhead does not hide behind or inflate the kernel time; HIP events on that
-stream bracket it, with a device synchronize on both sides.  Before that,
+stream bracket each replay, with a device synchronize on both sides, and the
+reported time is the median of 7 replays (min and max beside it, as the
+reference's harness reports them, tests/perf/harness.rs:62-120).  Before that,
 untimed warmup calls run for at least --warmup calls and --warmup-ms of wall
 time (300 ms by default): from idle the GPU takes some 100 ms of load to raise
 its clocks, and a shorter warmup times the ramp instead of the steady state.
 
-The other workloads of the path follow under "workloads": the requantizing
-int8 linear layer with a prepacked weight (2048 x 4096 x 11008, 16 calls per
-step), batched bf16 attention scores (64 x 512 x 512 x 128, f32 out), bf16
-4096^3 (the matrix-core-bound bf16 shape), int8 GEMV (W 14336 x 4096, M = 1
-and 8; five weight copies rotate so the 256 MB Infinity Cache cannot serve
-them), f32 GEMV 16384^2, the f32 512^3 case, bf16 4096^3 with a fused bias
-and ReLU, and prepacked weights at small batch (k = n = 2048, m = 8 and 64).
+The other workloads of the path follow under "workloads", each with its own
+roofline (achieved rate against the bound that limits it) and CPU baseline:
+the requantizing int8 linear layer with a prepacked weight (2048 x 4096 x
+11008, 16 calls per step), batched bf16 attention scores (64 x 512 x 512 x 128,
+f32 out; five input/output sets rotate so the 256 MB Infinity Cache cannot
+serve them), bf16 4096^3 (the matrix-core-bound bf16 shape), int8 GEMV (W
+14336 x 4096, M = 1 and 8; five weight copies rotate), f32 GEMV 16384^2, the f32
+512^3 case, bf16 4096^3 with a fused bias and ReLU, and prepacked weights at
+small batch (k = n = 2048, m = 8 and 64).
 
-roofline: algorithmic ops of one 4096^3 launch (2*4096^3) over the average
-launch time from the HIP events, against MI355X's published dense int8 peak
-(5.0 POP/s).  traffic: HBM bytes per launch from the committed rocprofv3
+roofline: algorithmic work of one launch (ops, or bytes for the HBM-bound
+shapes) over the median launch time from the HIP events, against MI355X's
+published peaks (int8 5.0 POP/s, bf16 2.5 PFLOP/s, f32 matrix 157.3 TFLOP/s,
+HBM 8 TB/s).  traffic: HBM bytes per call from the committed rocprofv3
 counter summary (profiles/traffic.json), or null.
 mfma_util: the headline kernel's matrix-core utilisation from the committed
-rocprofv3 counter summary (profiles/mfma_util.json): SQ_VALU_MFMA_BUSY_CYCLES
-over GRBM_GUI_ACTIVE per XCD times the 1024 SIMDs, i.e. busy against the
-clock the chip ran at under the counters (eager launches), or null.  The
-roofline's frac is the same kernel against the published 2.4 GHz peak.
-cpu_baseline: the oracle's C restatement of gemmkit's CPU i8 path (BLIS
-5-loop + AVX-512 VNNI microkernel, OpenMP threads) on the host cores, timed
-the way gemmkit's perf harness times (3 warmups, ~70 ms batches, median of 9).
+rocprofv3 counter summary (profiles/mfma_util.json), or null.
+cpu_baseline: the oracle's C restatement of gemmkit's CPU paths
+(oracle/cpu_port.c: BLIS 5-loop with the AVX-512 VNNI / FMA / BF16-dot
+microtiles, the dot_rows GEMV; OpenMP threads) on the host cores, Serial and
+all cores, timed the way gemmkit's perf harness times (3 warmups, batches
+calibrated to ~70 ms, median of up to 9), each leg bounded to a few seconds;
+where a Serial run of the whole workload would take longer, a stated sample
+of it is timed and the rate is over that sample's work.
 """
 from __future__ import annotations
 
@@ -46,6 +52,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK = {"int8": 5.0e15, "bf16": 2.5e15, "f32": 157.3e12, "hbm": 8.0e12}
+ROTATE = 5  # input/output sets cycled through for the HBM-bound workloads
 
 
 def parse():
@@ -127,6 +134,90 @@ class Timer:
         return med
 
 
+def roofline(bound: str, work: float, ms: float, traffic=None) -> dict:
+    """Achieved rate of `work` (ops, or bytes for bound "hbm") in `ms` against
+    the published peak of `bound` ("int8", "bf16", "f32" matrix, "hbm")."""
+    rate = work / (ms * 1e-3)
+    if bound == "hbm":
+        return {"bound": "hbm", "achieved": rate / 1e9, "peak": PEAK["hbm"] / 1e9, "unit": "GB/s",
+                "frac": rate / PEAK["hbm"], "traffic": traffic}
+    unit = "TOPS" if bound == "int8" else "TFLOP/s"
+    return {"bound": "mfma", "dtype": bound, "achieved": rate / 1e12, "peak": PEAK[bound] / 1e12,
+            "unit": unit, "frac": rate / PEAK[bound], "traffic": traffic}
+
+
+def load_traffic():
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return {}
+    with open(path) as f:
+        return json.load(f)
+
+
+# ---------------------------------------------------------------- CPU baseline
+
+def cpu_rate(run, work: float, budget_s: float, scale: float = 1e12):
+    """gemmkit's perf harness (tests/perf/harness.rs:32-120): 3 warmups, then
+    batches of calls calibrated to ~70 ms, the median rate of up to 9 batches
+    with min and max, stopping early when `budget_s` has passed.  Returns
+    (median, min, max, batches, calls per batch) in units of `scale`."""
+    t_end = time.perf_counter() + budget_s
+    t0 = time.perf_counter()
+    run()
+    one = time.perf_counter() - t0
+    for _ in range(2):
+        if time.perf_counter() + one > t_end:
+            break
+        run()
+    iters = max(1, int(0.07 / max(one, 1e-6)))
+    rates = []
+    while len(rates) < 9:
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            run()
+        dt = (time.perf_counter() - t0) / iters
+        rates.append(work / dt / scale)
+        if time.perf_counter() + dt * iters > t_end and len(rates) >= 3:
+            break
+    rates.sort()
+    return rates[len(rates) // 2], rates[0], rates[-1], len(rates), iters
+
+
+def cpu_legs(legs, unit: str, scale: float, oracle):
+    """legs: {"serial": (run, work, budget_s, sample), "all_cores": ...}, each
+    `run` a callable taking the thread count.  Returns the baseline object:
+    all-cores figures at the top level (value/unit/cores/kind/sample) and the
+    Serial leg under "serial"."""
+    out = {}
+    nt = oracle.port_max_threads()
+    for name, (run, work, budget, sample) in legs.items():
+        threads = 1 if name == "serial" else nt
+        med, lo, hi, nb, it = cpu_rate(lambda: run(threads), work, budget, scale)
+        out[name] = {"value": med, "unit": unit, "cores": threads, "kind": "port",
+                     "sample": f"{sample}; {nb} batches of {it}; median; min {lo:.4g} "
+                               f"max {hi:.4g}"}
+    top = dict(out.get("all_cores", {}))
+    if "serial" in out:
+        top["serial"] = out["serial"]
+    isa = (f"AVX-512F={'yes' if oracle.port_has_avx512f() else 'no'}, "
+           f"VNNI={'yes' if oracle.port_has_vnni() else 'no'}, "
+           f"BF16={'yes' if oracle.port_has_bf16() else 'no'}")
+    top["host_isa"] = isa
+    top["host_cpu"] = host_cpu()
+    return top
+
+
+def host_cpu() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -144,13 +235,16 @@ def main():
     timed = Timer(args.eager, args.warmup_ms)
     props = torch.cuda.get_device_properties(0)
     workloads = {}
+    traffic_all = load_traffic()
+    cpu_on = not args.no_cpu_baseline and args.only is None
+    oracle = None
+    if cpu_on or args.only in (None, "i8_gemm_4096"):
+        import oracle  # the checker and the CPU-baseline port (test infrastructure)
 
     def want(name):
         return args.only is None or args.only == name
 
-    need_oracle = args.only is None or args.only == "i8_gemm_4096"
-    if need_oracle:
-        import oracle
+    if oracle is not None:
         gen_a = oracle.rng_i8_full(1, 4096 * 4096)
         gen_b = oracle.rng_i8_full(2, 4096 * 4096)
     else:
@@ -160,6 +254,7 @@ def main():
 
     # ---------------------------------------------------------------- headline
     M = N = K = 4096
+    ops = 2 * M * N * K
     ad = torch.from_numpy(gen_a).to(dev)
     bd = torch.from_numpy(gen_b).to(dev)
     cd = torch.empty(M * N, dtype=torch.int32, device=dev)
@@ -167,8 +262,8 @@ def main():
     if want("i8_gemm_4096"):
         call = lambda: gk.gemm_i8_unchecked(M, K, N, 1, ad, K, 1, bd, 1, K, 0, cd, N, 1)  # noqa: E731
         i8_ms = timed(call, args.steps, args.warmup)
-        entry = {"ms": i8_ms, "TOPS": 2 * M * N * K / i8_ms / 1e9, **timed.last}
-        if need_oracle:
+        entry = {"ms": i8_ms, "TOPS": ops / i8_ms / 1e9, **timed.last}
+        if oracle is not None:
             # spot check the timed output: row 17 against the oracle
             ref = np.zeros(N, np.int32)
             oracle.gemm_i8(1, K, N, 1, gen_a[17 * K:18 * K], K, 1, gen_b, 1, K, 0, ref, N, 1)
@@ -178,20 +273,28 @@ def main():
 
     # ------------------------------------------------------------------ extras
     if not args.no_extra:
-        run_extras(args, workloads, want, timed, dev, gk, np, torch)
+        run_extras(args, workloads, want, timed, dev, gk, np, torch, traffic_all,
+                   oracle if cpu_on else None)
 
     # ------------------------------------------------------------ CPU baseline
     cpu = None
-    if not args.no_cpu_baseline and args.only is None:
-        cpu = cpu_baseline(oracle, np, gen_a, gen_b, M, N, K)
+    if cpu_on:
+        c_host = np.empty(M * N, np.int32)
+        rows_s = 512  # Serial: the first 512 rows of A against all of B
 
-    ops = 2 * M * N * K
+        def run_i8(threads, rows=M):
+            oracle.port_gemm_i8(rows, K, N, 1, gen_a, K, 1, gen_b, 1, K, 0, c_host, N, 1, threads)
+
+        cpu = cpu_legs({
+            "all_cores": (run_i8, ops, 20.0,
+                          "full 4096^3 gemm_i8 (A row-major, B col-major) on the same inputs"),
+            "serial": (lambda t: run_i8(t, rows_s), 2 * rows_s * N * K, 10.0,
+                       f"the first {rows_s} rows of A (1/8 of the work) against the full B"),
+        }, "TOPS", 1e12, oracle)
+        workloads.setdefault("i8_gemm_4096", {})["cpu_baseline"] = cpu
+
     value = ops / (i8_ms * 1e-3) / 1e12 if i8_ms else None
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "traffic.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get("i8_gemm_4096", {}).get("hbm_bytes_per_launch")
+    traffic = traffic_all.get("i8_gemm_4096", {}).get("hbm_bytes_per_launch")
     mfma_util = None
     upath = os.path.join(ROOT, "profiles", "mfma_util.json")
     if os.path.exists(upath):
@@ -218,7 +321,8 @@ def main():
         "config": {"workload": "gemm_i8 M=N=K=4096, A row-major, B col-major via strides, "
                                "C row-major i32, alpha=1, beta=0",
                    "device": props.name, "cus": props.multi_processor_count,
-                   "timing": "eager" if args.eager else "hip graph of the K calls"},
+                   "timing": ("eager" if args.eager else "hip graph of the K calls") +
+                             ", median of 7 replays"},
         "roofline": {"bound": "mfma", "achieved": value, "peak": PEAK["int8"] / 1e12,
                      "unit": "TOPS", "frac": (value * 1e12 / PEAK["int8"]) if value else None,
                      "traffic": traffic},
@@ -229,13 +333,21 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def run_extras(args, workloads, want, timed, dev, gk, np, torch):
+def run_extras(args, workloads, want, timed, dev, gk, np, torch, traffic_all, oracle):
+    """The other workloads of the path; `oracle` (the CPU port) is None when
+    the CPU baselines are off."""
     steps = max(5, args.steps // 2)
     warm = max(2, args.warmup // 2)
     g = torch.Generator(device="cpu").manual_seed(7)
 
     def i8(n):
         return torch.randint(-127, 128, (n,), dtype=torch.int8, generator=g).to(dev)
+
+    def tr(name):
+        return traffic_all.get(name, {}).get("hbm_bytes_per_launch")
+
+    def host(t):
+        return np.ascontiguousarray(t.cpu().numpy())
 
     # int8 linear layer + requant, W prepacked once, 16 calls per step
     if want("i8_layer_requant"):
@@ -250,28 +362,61 @@ def run_extras(args, workloads, want, timed, dev, gk, np, torch):
             T, x, K, 1, packed, 0.0, scale, 0, bias, y, Nc, 1, axis=1, relu=True)
         ms = timed(call, 16 * max(1, steps // 8), 2)
         ops = 2 * T * K * Nc
-        workloads["i8_layer_requant"] = {"ms_per_call": ms, "calls_per_step": 16, **timed.last,
-                                         "TOPS": ops / ms / 1e9,
-                                         "frac_int8_peak": ops / (ms * 1e-3) / 5.0e15}
+        e = {"ms_per_call": ms, "calls_per_step": 16, **timed.last, "TOPS": ops / ms / 1e9,
+             "frac_int8_peak": ops / (ms * 1e-3) / PEAK["int8"],
+             "roofline": roofline("int8", ops, ms, tr("i8_layer_requant"))}
+        if oracle is not None:
+            xh, wh, bh, sh = host(x), host(w), host(bias), host(scale)
+            yh = np.empty(T * Nc, np.uint8)
+            pb = oracle.PortPackedB(K, Nc, wh, 1, K)
+            ts = 256  # Serial: 256 tokens
+
+            def run(threads, tokens=T):
+                oracle.port_gemm_i8_requant(tokens, K, Nc, xh, K, 1, None, 0, 0, 0.0, sh, 0, bh,
+                                            1, 0, 127, yh, Nc, 1, threads, packed=pb)
+            e["cpu_baseline"] = cpu_legs({
+                "all_cores": (run, ops, 8.0, "the full layer per call (2048 tokens) on the same "
+                                             "inputs, W prepacked once"),
+                "serial": (lambda t: run(t, ts), 2 * ts * K * Nc, 6.0,
+                           f"the first {ts} tokens (1/8 of a call) on the same prepacked W"),
+            }, "TOPS", 1e12, oracle)
+            del pb
+        workloads["i8_layer_requant"] = e
         del x, w, y, packed
 
-    # batched bf16 attention scores, f32 out
+    # batched bf16 attention scores, f32 out; ROTATE sets cycle (84 MB each)
     if want("bf16_batched_attn"):
         Bt, S, D = 64, 512, 128
-        q = torch.randn(Bt * S * D, generator=g).to(torch.bfloat16).to(dev)
-        kk = torch.randn(Bt * S * D, generator=g).to(torch.bfloat16).to(dev)
-        out = torch.empty(Bt * S * S, dtype=torch.float32, device=dev)
+        sets = []
+        for _ in range(ROTATE):
+            q = torch.randn(Bt * S * D, generator=g).to(torch.bfloat16).to(dev)
+            kk = torch.randn(Bt * S * D, generator=g).to(torch.bfloat16).to(dev)
+            out = torch.empty(Bt * S * S, dtype=torch.float32, device=dev)
+            sets.append((q, kk, out))
         alpha = 1.0 / np.sqrt(128.0)
-        call = lambda: gk.gemm_batched_bf16_f32out(  # noqa: E731
+        calls = [lambda q=q, kk=kk, out=out: gk.gemm_batched_bf16_f32out(
             Bt, alpha, gk.MatRef.from_row_major(q, S, D), S * D, gk.MatRef(kk, D, S, 1, D), S * D,
-            0.0, gk.MatMut.from_row_major(out, S, S), S * S)
-        ms = timed(call, steps, warm)
+            0.0, gk.MatMut.from_row_major(out, S, S), S * S) for q, kk, out in sets]
+        ms = timed(calls, 10 * len(calls), warm)
         byts = 2 * Bt * S * D * 2 + Bt * S * S * 4
-        workloads["bf16_batched_attn"] = {"ms": ms, **timed.last,
-                                          "TFLOPS": 2 * Bt * S * S * D / ms / 1e9,
-                                          "GBps": byts / ms / 1e6,
-                                          "frac_hbm": byts / (ms * 1e-3) / 8.0e12}
-        del q, kk, out
+        flops = 2 * Bt * S * S * D
+        e = {"ms": ms, **timed.last, "sets_rotated": ROTATE, "TFLOPS": flops / ms / 1e9,
+             "GBps": byts / ms / 1e6, "frac_hbm": byts / (ms * 1e-3) / PEAK["hbm"],
+             "roofline": roofline("hbm", byts, ms, tr("bf16_batched_attn"))}
+        if oracle is not None:
+            qh = host(sets[0][0].view(torch.int16)).view(np.uint16)
+            kh = host(sets[0][1].view(torch.int16)).view(np.uint16)
+            oh = np.empty(Bt * S * S, np.float32)
+
+            def run(threads):
+                oracle.port_gemm_batched_bf16_f32out(Bt, S, D, S, alpha, qh, D, 1, S * D, kh, 1,
+                                                     D, S * D, 0.0, oh, S, 1, S * S, threads)
+            sample = "the full batch (64 x 512 x 512 x 128) on the first input set"
+            e["cpu_baseline"] = cpu_legs({"all_cores": (run, flops, 6.0, sample),
+                                          "serial": (run, flops, 6.0, sample)},
+                                         "TFLOP/s", 1e12, oracle)
+        workloads["bf16_batched_attn"] = e
+        del sets
 
     # bf16 4096^3 (matrix-core bound), f32 out
     if want("bf16_gemm_4096"):
@@ -283,14 +428,31 @@ def run_extras(args, workloads, want, timed, dev, gk, np, torch):
                                            gk.MatRef(b, n, n, 1, n), 0.0,
                                            gk.MatMut.from_row_major(c, n, n))
         ms = timed(call, steps, warm)
-        workloads["bf16_gemm_4096"] = {"ms": ms, **timed.last, "TFLOPS": 2 * n ** 3 / ms / 1e9,
-                                       "frac_bf16_peak": 2 * n ** 3 / (ms * 1e-3) / 2.5e15}
+        flops = 2 * n ** 3
+        e = {"ms": ms, **timed.last, "TFLOPS": flops / ms / 1e9,
+             "frac_bf16_peak": flops / (ms * 1e-3) / PEAK["bf16"],
+             "roofline": roofline("bf16", flops, ms, tr("bf16_gemm_4096"))}
+        if oracle is not None:
+            ah = host(a.view(torch.int16)).view(np.uint16)
+            bh = host(b.view(torch.int16)).view(np.uint16)
+            ch = np.empty(n * n, np.float32)
+
+            def run(threads, rows=n):
+                oracle.port_gemm_batched_bf16_f32out(1, rows, n, n, 1.0, ah, n, 1, 0, bh, 1, n, 0,
+                                                     0.0, ch, n, 1, 0, threads)
+            rs = 256
+            e["cpu_baseline"] = cpu_legs({
+                "all_cores": (run, flops, 8.0, "full 4096^3 bf16 -> f32 on the same inputs"),
+                "serial": (lambda t: run(t, rs), 2 * rs * n * n, 6.0,
+                           f"the first {rs} rows of A (1/16 of the work) against the full B"),
+            }, "TFLOP/s", 1e12, oracle)
+        workloads["bf16_gemm_4096"] = e
         del a, b, c
 
-    # int8 GEMV, W 14336 x 4096, M = 1 and 8; five weight copies rotate
+    # int8 GEMV, W 14336 x 4096, M = 1 and 8; ROTATE weight copies
     if want("i8_gemv"):
         Nw, K = 14336, 4096
-        copies = [i8(Nw * K) for _ in range(5)]
+        copies = [i8(Nw * K) for _ in range(ROTATE)]
         for Mv in (1, 8):
             x = i8(Mv * K)
             y = torch.empty(Mv * Nw, dtype=torch.int32, device=dev)
@@ -298,8 +460,22 @@ def run_extras(args, workloads, want, timed, dev, gk, np, torch):
                      for w in copies]
             ms = timed(calls, 10 * len(calls), warm)
             byts = Nw * K + Mv * K + Mv * Nw * 4
-            workloads[f"i8_gemv_m{Mv}"] = {"ms": ms, **timed.last, "GBps": byts / ms / 1e6,
-                                           "frac_hbm": byts / (ms * 1e-3) / 8.0e12}
+            name = f"i8_gemv_m{Mv}"
+            e = {"ms": ms, **timed.last, "GBps": byts / ms / 1e6,
+                 "frac_hbm": byts / (ms * 1e-3) / PEAK["hbm"],
+                 "roofline": roofline("hbm", byts, ms, tr(name))}
+            if oracle is not None:
+                xh, wh = host(x), host(copies[0])
+                yh = np.empty(Mv * Nw, np.int32)
+
+                def run(threads):
+                    oracle.port_gemm_i8(Mv, K, Nw, 1, xh, K, 1, wh, 1, K, 0, yh, Nw, 1, threads)
+                sample = (f"the full product (M = {Mv}) through the CPU i8 GEMM, which packs the "
+                          "weight every call as the reference's gemm_i8 does")
+                e["cpu_baseline"] = cpu_legs({"all_cores": (run, byts, 4.0, sample),
+                                              "serial": (run, byts, 4.0, sample)},
+                                             "GB/s", 1e9, oracle)
+            workloads[name] = e
         del copies
 
     # f32 GEMV 16384^2 (1 GiB matrix, larger than the Infinity Cache)
@@ -311,8 +487,21 @@ def run_extras(args, workloads, want, timed, dev, gk, np, torch):
         call = lambda: gk.gemm_unchecked(n, n, 1, 1.0, A, n, 1, xv, 1, 1, 0.0, yv, 1, 1)  # noqa: E731
         ms = timed(call, steps, warm)
         byts = n * n * 4 + n * 4 + n * 4
-        workloads["f32_gemv_16384"] = {"ms": ms, **timed.last, "GBps": byts / ms / 1e6,
-                                       "frac_hbm": byts / (ms * 1e-3) / 8.0e12}
+        e = {"ms": ms, **timed.last, "GBps": byts / ms / 1e6,
+             "frac_hbm": byts / (ms * 1e-3) / PEAK["hbm"],
+             "roofline": roofline("hbm", byts, ms, tr("f32_gemv_16384"))}
+        if oracle is not None:
+            Ah, xh = host(A), host(xv)
+            yh = np.empty(n, np.float32)
+
+            def run(threads):
+                oracle.port_gemv_f32(n, n, 1.0, Ah, n, xh, 0.0, yh, 1, threads)
+            sample = "the full 16384^2 GEMV on the same inputs (dot_rows, rows across threads)"
+            e["cpu_baseline"] = cpu_legs({"all_cores": (run, byts, 5.0, sample),
+                                          "serial": (run, byts, 5.0, sample)},
+                                         "GB/s", 1e9, oracle)
+            del Ah
+        workloads["f32_gemv_16384"] = e
         del A
 
     # f32 512^3 (all row-major; B goes through the pack into k-contiguous form)
@@ -323,7 +512,20 @@ def run_extras(args, workloads, want, timed, dev, gk, np, torch):
         c = torch.empty(n * n, device=dev)
         call = lambda: gk.gemm_unchecked(n, n, n, 1.0, a, n, 1, b, n, 1, 0.0, c, n, 1)  # noqa: E731
         ms = timed(call, steps, warm)
-        workloads["f32_gemm_512"] = {"ms": ms, **timed.last, "TFLOPS": 2 * n ** 3 / ms / 1e9}
+        flops = 2 * n ** 3
+        e = {"ms": ms, **timed.last, "TFLOPS": flops / ms / 1e9,
+             "roofline": roofline("f32", flops, ms, tr("f32_gemm_512"))}
+        if oracle is not None:
+            ah, bh = host(a), host(b)
+            ch = np.empty(n * n, np.float32)
+
+            def run(threads):
+                oracle.port_gemm_f32(n, n, n, 1.0, ah, n, 1, bh, n, 1, 0.0, ch, n, 1, threads)
+            sample = "the full 512^3 f32 product (all row-major) on the same inputs"
+            e["cpu_baseline"] = cpu_legs({"all_cores": (run, flops, 3.0, sample),
+                                          "serial": (run, flops, 3.0, sample)},
+                                         "TFLOP/s", 1e12, oracle)
+        workloads["f32_gemm_512"] = e
 
     # bf16 4096^3 with bf16 output: plain, and fused with a per-column bias and
     # ReLU (the epilogue's cost is the difference)
@@ -340,7 +542,8 @@ def run_extras(args, workloads, want, timed, dev, gk, np, torch):
                                             gk.Activation.Relu), steps, warm)
         workloads["bf16_fused_4096"] = {"ms_plain": plain, "ms_fused": fused,
                                         "TFLOPS_fused": 2 * n ** 3 / fused / 1e9,
-                                        "frac_bf16_peak": 2 * n ** 3 / (fused * 1e-3) / 2.5e15}
+                                        "frac_bf16_peak": 2 * n ** 3 / (fused * 1e-3) / 2.5e15,
+                                        "roofline": roofline("bf16", 2 * n ** 3, fused)}
         del a, b, c
 
     # prepacked weight at small batch (k = n = 2048, m = 8 and 64; A and C
@@ -383,36 +586,6 @@ def run_extras(args, workloads, want, timed, dev, gk, np, torch):
         dst = torch.empty_like(src)
         ms = timed(lambda: torch.neg(src, out=dst), steps, warm)
         workloads["copy_1gib"] = {"ms": ms, "GBps": 2 * (1 << 30) / ms / 1e6}
-
-
-def cpu_baseline(oracle, np, a, b, M, N, K):
-    """gemmkit's CPU i8 path restated in C (oracle/cpu_port.c), timed as the
-    reference's perf harness does: 3 warmups, batches calibrated to ~70 ms,
-    median of 9 (tests/perf/harness.rs:32-120).  Bounded to ~20 s."""
-    c = np.empty(M * N, np.int32)
-    threads = oracle.port_max_threads()
-    run = lambda: oracle.port_gemm_i8(M, K, N, 1, a, K, 1, b, 1, K, 0, c, N, 1, threads)  # noqa: E731
-    for _ in range(3):
-        run()
-    t0 = time.perf_counter()
-    run()
-    one = time.perf_counter() - t0
-    iters = max(1, int(0.07 / max(one, 1e-6)))
-    rates = []
-    deadline = time.perf_counter() + 20.0
-    for _ in range(9):
-        t0 = time.perf_counter()
-        for _ in range(iters):
-            run()
-        dt = (time.perf_counter() - t0) / iters
-        rates.append(2 * M * N * K / dt / 1e12)
-        if time.perf_counter() > deadline:
-            break
-    rates.sort()
-    return {"value": rates[len(rates) // 2], "unit": "TOPS", "cores": threads, "kind": "port",
-            "sample": f"full 4096^3 gemm_i8 (A row-major, B col-major) on the same inputs, "
-                      f"{len(rates)} batches of {iters}; median; min {rates[0]:.3f} max "
-                      f"{rates[-1]:.3f}; AVX-512 VNNI={'yes' if oracle.port_has_vnni() else 'no'}"}
 
 
 if __name__ == "__main__":

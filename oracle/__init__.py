@@ -284,11 +284,33 @@ def fused_map_bf16(v: np.ndarray, bias_bits=None, dim: int = 0, act: int = 0,
 def _port() -> C.CDLL:
     lib = _lib("libcpu_port.so")
     if not getattr(lib, "_typed", False):
+        vp = C.c_void_p
+        f32p = C.POINTER(C.c_float)
+        u16p = C.POINTER(C.c_uint16)
+        u8p = C.POINTER(C.c_uint8)
         lib.port_gemm_i8.argtypes = [_sz, _sz, _sz, C.c_int32, _i8p, _sd, _sd, _i8p, _sd, _sd,
                                      C.c_int32, _i32p, _sd, _sd, C.c_int]
         lib.port_gemm_i8.restype = C.c_int
-        lib.port_has_vnni.restype = C.c_int
-        lib.port_max_threads.restype = C.c_int
+        lib.port_prepack_b_i8.argtypes = [_sz, _sz, _i8p, _sd, _sd, C.c_int]
+        lib.port_prepack_b_i8.restype = vp
+        lib.port_packed_b_free.argtypes = [vp]
+        lib.port_packed_b_free.restype = None
+        lib.port_gemm_i8_requant.argtypes = [_sz, _sz, _sz, _i8p, _sd, _sd, _i8p, _sd, _sd, vp,
+                                             C.c_float, f32p, C.c_int32, _i32p, C.c_int,
+                                             C.c_int32, C.c_int32, u8p, _sd, _sd, C.c_int]
+        lib.port_gemm_i8_requant.restype = C.c_int
+        lib.port_gemm_f32.argtypes = [_sz, _sz, _sz, C.c_float, f32p, _sd, _sd, f32p, _sd, _sd,
+                                      C.c_float, f32p, _sd, _sd, C.c_int]
+        lib.port_gemm_f32.restype = C.c_int
+        lib.port_gemm_batched_bf16_f32out.argtypes = [_sz, _sz, _sz, _sz, C.c_float, u16p, _sd,
+                                                      _sd, _sd, u16p, _sd, _sd, _sd, C.c_float,
+                                                      f32p, _sd, _sd, _sd, C.c_int]
+        lib.port_gemm_batched_bf16_f32out.restype = C.c_int
+        lib.port_gemv_f32.argtypes = [_sz, _sz, C.c_float, f32p, _sd, f32p, C.c_float, f32p,
+                                      _sd, C.c_int]
+        lib.port_gemv_f32.restype = C.c_int
+        for name in ("port_has_vnni", "port_has_avx512f", "port_has_bf16", "port_max_threads"):
+            getattr(lib, name).restype = C.c_int
         lib._typed = True
     return lib
 
@@ -300,8 +322,69 @@ def port_gemm_i8(m, k, n, alpha, a, rsa, csa, b, rsb, csb, beta, c, rsc, csc,
                                 rsb, csb, int(beta), _ptr(c, _i32p), rsc, csc, int(threads))
 
 
+class PortPackedB:
+    """A B operand packed once in the VNNI panel layout (port_prepack_b_i8)."""
+
+    def __init__(self, k, n, b, rsb, csb, threads: int = 0):
+        self._keep = b
+        self.k, self.n = k, n
+        self.h = _port().port_prepack_b_i8(k, n, _ptr(b, _i8p), rsb, csb, int(threads))
+
+    def __del__(self):
+        h, self.h = getattr(self, "h", None), None
+        if h:
+            _port().port_packed_b_free(h)
+
+
+def port_gemm_i8_requant(m, k, n, a, rsa, csa, b, rsb, csb, scale, scales, zp, bias, axis,
+                         lo, hi, c, rsc, csc, threads: int = 0, packed: PortPackedB = None) -> int:
+    """gemmkit's requantizing VNNI path restated (kc = k, map per drained tile);
+    `packed` replaces b.  Same argument meaning as gemm_i8_requant below."""
+    f32p = C.POINTER(C.c_float)
+    return _port().port_gemm_i8_requant(
+        m, k, n, _ptr(a, _i8p), rsa, csa, None if packed is not None else _ptr(b, _i8p), rsb,
+        csb, packed.h if packed is not None else None, float(scale),
+        None if scales is None else _ptr(scales, f32p), int(zp),
+        None if bias is None else _ptr(bias, _i32p), int(axis), int(lo), int(hi),
+        _ptr(c, C.POINTER(C.c_uint8)), rsc, csc, int(threads))
+
+
+def port_gemm_f32(m, k, n, alpha, a, rsa, csa, b, rsb, csb, beta, c, rsc, csc,
+                  threads: int = 0) -> int:
+    """gemmkit's f32 path restated (BLIS + AVX-512F 32x12 FMA microtile)."""
+    f32p = C.POINTER(C.c_float)
+    return _port().port_gemm_f32(m, k, n, float(alpha), _ptr(a, f32p), rsa, csa, _ptr(b, f32p),
+                                 rsb, csb, float(beta), _ptr(c, f32p), rsc, csc, int(threads))
+
+
+def port_gemm_batched_bf16_f32out(batch, m, k, n, alpha, a_bits, rsa, csa, a_bs, b_bits, rsb,
+                                  csb, b_bs, beta, c, rsc, csc, c_bs, threads: int = 0) -> int:
+    """gemmkit's bf16 dot path (vdpbf16ps, f32 accumulation) over a batch, f32
+    output; a_bits/b_bits are the bf16 bit patterns (uint16)."""
+    f32p = C.POINTER(C.c_float)
+    u16p = C.POINTER(C.c_uint16)
+    return _port().port_gemm_batched_bf16_f32out(
+        batch, m, k, n, float(alpha), _ptr(a_bits, u16p), rsa, csa, a_bs, _ptr(b_bits, u16p),
+        rsb, csb, b_bs, float(beta), _ptr(c, f32p), rsc, csc, c_bs, int(threads))
+
+
+def port_gemv_f32(rows, k, alpha, a, lda, x, beta, y, ys=1, threads: int = 0) -> int:
+    """gemmkit's row-partitioned f32 GEMV (dot_rows) restated."""
+    f32p = C.POINTER(C.c_float)
+    return _port().port_gemv_f32(rows, k, float(alpha), _ptr(a, f32p), lda, _ptr(x, f32p),
+                                 float(beta), _ptr(y, f32p), ys, int(threads))
+
+
 def port_has_vnni() -> bool:
     return bool(_port().port_has_vnni())
+
+
+def port_has_avx512f() -> bool:
+    return bool(_port().port_has_avx512f())
+
+
+def port_has_bf16() -> bool:
+    return bool(_port().port_has_bf16())
 
 
 def port_max_threads() -> int:

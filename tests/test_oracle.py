@@ -313,3 +313,94 @@ def test_generators_are_reproducible():
     assert y.min() == -127 and y.max() == 127
     u = oracle.rng_unit(5, 100000)
     assert -1 <= u.min() and u.max() < 1
+
+
+# The other CPU-port families, pinned against the oracle's closed forms:
+# bit-exact for the requantizing path, within the float bars for f32/bf16.
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (33, 17, 19), (100, 300, 50), (70, 1024, 129)])
+@pytest.mark.parametrize("axis", [0, 1])
+@pytest.mark.parametrize("row_major_c", [True, False])
+def test_cpu_port_requant_bit_exact(m, k, n, axis, row_major_c):
+    a = oracle.rng_i8_sym127(30 + m, m * k)
+    b = oracle.rng_i8_sym127(40 + n, k * n)  # B column-major (rsb = 1, csb = k)
+    ch = m if axis == 0 else n
+    scales = (1e-4 + (np.arange(ch) % 13) * 7.7e-4).astype(np.float32)
+    bias = ((np.arange(ch) * 7919) % 131073 - 65536).astype(np.int32)
+    rsc, csc = (n, 1) if row_major_c else (1, m)
+    for zp, lo, hi in [(0, 0, 127), (3, -128, 127), (-5, -128, 127)]:
+        want = np.zeros(m * n, np.int8)
+        oracle.gemm_i8_requant(m, k, n, a, k, 1, b, 1, k, 0.0, scales, zp, bias, axis, lo, hi,
+                               want, rsc, csc)
+        got = np.zeros(m * n, np.int8)
+        oracle.port_gemm_i8_requant(m, k, n, a, k, 1, b, 1, k, 0.0, scales, zp, bias, axis, lo,
+                                    hi, got.view(np.uint8), rsc, csc, threads=2)
+        assert np.array_equal(got, want), (zp, lo, hi)
+        # the same with B prepacked once (no orientation swap: C as given)
+        pb = oracle.PortPackedB(k, n, b, 1, k, threads=2)
+        got2 = np.zeros(m * n, np.int8)
+        oracle.port_gemm_i8_requant(m, k, n, a, k, 1, None, 0, 0, 0.0, scales, zp, bias, axis,
+                                    lo, hi, got2.view(np.uint8), rsc, csc, threads=2, packed=pb)
+        assert np.array_equal(got2, want), ("packed", zp, lo, hi)
+
+
+def test_cpu_port_requant_per_tensor_scale():
+    m, k, n = 40, 96, 30
+    a = oracle.rng_i8_full(51, m * k)
+    b = oracle.rng_i8_full(52, k * n)
+    want = np.zeros(m * n, np.int8)
+    oracle.gemm_i8_requant(m, k, n, a, k, 1, b, 1, k, 0.003, None, 1, None, 0, -128, 127, want,
+                           n, 1)
+    got = np.zeros(m * n, np.int8)
+    oracle.port_gemm_i8_requant(m, k, n, a, k, 1, b, 1, k, 0.003, None, 1, None, 0, -128, 127,
+                                got.view(np.uint8), n, 1, threads=3)
+    assert np.array_equal(got, want)
+
+
+def _rel_frob(got, ref):
+    return np.linalg.norm(got.astype(np.float64) - ref) / np.linalg.norm(ref)
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (33, 17, 19), (100, 300, 50), (257, 1024, 129),
+                                   (512, 512, 512)])
+@pytest.mark.parametrize("alpha,beta", [(1.0, 0.0), (0.5, 1.0), (2.0, -0.75)])
+@pytest.mark.parametrize("row_major_c", [True, False])
+def test_cpu_port_f32_within_tolerance(m, k, n, alpha, beta, row_major_c):
+    a = oracle.rand_vec(60 + m, m * k).astype(np.float32)
+    b = oracle.rand_vec(70 + n, k * n).astype(np.float32)
+    rsc, csc = (n, 1) if row_major_c else (1, m)
+    c0 = oracle.rand_vec(80, m * n).astype(np.float32)
+    ref = oracle.gemm_f64(m, k, n, alpha, a, k, 1, b, n, 1, beta, c0.astype(np.float64), rsc,
+                          csc)
+    got = c0.copy()
+    oracle.port_gemm_f32(m, k, n, alpha, a, k, 1, b, n, 1, beta, got, rsc, csc, threads=2)
+    dense = got.reshape(m, n) if row_major_c else got.reshape(n, m).T
+    assert _rel_frob(dense, ref) <= 1e-5
+
+
+@pytest.mark.parametrize("batch,m,k,n", [(1, 33, 17, 19), (3, 64, 128, 64), (5, 100, 130, 70)])
+def test_cpu_port_bf16_within_tolerance(batch, m, k, n):
+    a = oracle.bf16_bits(oracle.rng_normal(90, batch * m * k).astype(np.float32))
+    b = oracle.bf16_bits(oracle.rng_normal(91, batch * k * n).astype(np.float32))
+    af = oracle.bf16_to_f32(a).astype(np.float64).reshape(batch, m, k)
+    bf = oracle.bf16_to_f32(b).astype(np.float64).reshape(batch, n, k)  # B column-major
+    alpha = 1.0 / np.sqrt(128.0)
+    ref = alpha * np.einsum("zik,zjk->zij", af, bf)
+    got = np.zeros(batch * m * n, np.float32)
+    oracle.port_gemm_batched_bf16_f32out(batch, m, k, n, alpha, a, k, 1, m * k, b, 1, k, k * n,
+                                         0.0, got, n, 1, m * n, threads=2)
+    assert _rel_frob(got, ref.ravel()) <= 1e-5
+    err = np.abs(got.astype(np.float64) - ref.ravel())
+    assert (err <= 1e-2 * np.maximum(np.abs(ref.ravel()), 1e-3 * np.abs(ref).max())).all()
+
+
+@pytest.mark.parametrize("rows,k", [(1, 1), (7, 33), (100, 1000), (1027, 4099)])
+@pytest.mark.parametrize("beta", [0.0, 0.5])
+def test_cpu_port_gemv_within_tolerance(rows, k, beta):
+    a = oracle.rand_vec(100 + rows, rows * k).astype(np.float32)
+    x = oracle.rand_vec(101, k).astype(np.float32)
+    y0 = oracle.rand_vec(102, rows).astype(np.float32)
+    ref = oracle.gemv_f64(rows, k, 1.25, a, k, 1, x, 1, beta, y0.astype(np.float64), 1)
+    got = y0.copy()
+    oracle.port_gemv_f32(rows, k, 1.25, a, k, x, beta, got, 1, threads=3)
+    assert _rel_frob(got, ref) <= 1e-5
