@@ -81,17 +81,20 @@ struct Mma<InType::F32> {
     }
 };
 
-// Workgroup id -> (tile_m, tile_n).  The hardware hands consecutive workgroup
-// ids to the 8 XCDs round-robin; the first remap gives every XCD one
-// contiguous range of logical ids, and the grouped order below makes each
-// range a compact block of tiles, so the A rows and B columns it needs stay in
-// that XCD's L2.
-__device__ __forceinline__ void tile_coords(int bid, int nblocks, int tiles_m, int tiles_n,
-                                            int &tm, int &tn) {
-    const int X = 8;
-    int per = nblocks / X, rem = nblocks % X;
-    int xcd = bid % X, idx = bid / X;
-    int pid = xcd * per + (xcd < rem ? xcd : rem) + idx;
+// The hardware hands consecutive workgroups (in x, then y, then z order) to
+// the 8 XCDs round-robin.  This gives every XCD one contiguous range of
+// logical ids instead: workgroup `bid` of `nblocks` -> logical id.
+__device__ __forceinline__ int64_t xcd_logical(int64_t bid, int64_t nblocks) {
+    const int64_t X = 8;
+    const int64_t per = nblocks / X, rem = nblocks % X;
+    const int64_t xcd = bid % X, idx = bid / X;
+    return xcd * per + (xcd < rem ? xcd : rem) + idx;
+}
+
+// Logical tile id -> (tile_m, tile_n).  The grouped order makes each XCD's
+// contiguous range a compact block of tiles, so the A rows and B columns it
+// needs stay in that XCD's L2.
+__device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, int &tm, int &tn) {
     const int G = 8;
     int in_group = G * tiles_n;
     int group = pid / in_group;
@@ -265,15 +268,27 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
 
     const int tiles_m = (args.M + BM - 1) / BM;
     const int tiles_n = (args.N + BN - 1) / BN;
+    // Batch element zb, output slab z.  A batched launch remaps (tile, element)
+    // pairs as one range, so the few tiles of an element share an XCD (and its
+    // L2 copy of the element's operands).  SPLIT: K range blockIdx.y, and each
+    // range's partial sums go to a slab of their own, z = zb * splits + range
+    // (the epilogue's batch stride), to be reduced in range order afterwards.
+    // The unsplit kernels are separate instantiations, so their code is
+    // untouched by this.  Which workgroup computes a tile does not change its
+    // arithmetic.
+    int64_t zb = blockIdx.z;
+    int tid_logical;
+    if (!SPLIT && gridDim.z > 1) {
+        const int64_t pid = xcd_logical((int64_t)blockIdx.z * gridDim.x + blockIdx.x,
+                                        (int64_t)gridDim.x * gridDim.z);
+        zb = pid / gridDim.x;
+        tid_logical = (int)(pid % gridDim.x);
+    } else {
+        tid_logical = (int)xcd_logical(blockIdx.x, gridDim.x);
+    }
     int tmi, tni;
-    tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tmi, tni);
+    tile_coords(tid_logical, tiles_m, tiles_n, tmi, tni);
     const int m0 = tmi * BM, n0 = tni * BN;
-    // Batch element zb = blockIdx.z, output slab z.  SPLIT: K range
-    // blockIdx.y, and each range's partial sums go to a slab of their own,
-    // z = zb * splits + range (the epilogue's batch stride), to be reduced in
-    // range order afterwards.  The unsplit kernels are separate
-    // instantiations, so their code is untouched by this.
-    const int64_t zb = blockIdx.z;
     int64_t z = zb, k0 = 0, kel = args.K;
     if constexpr (SPLIT) {
         z = zb * args.splits + blockIdx.y;
