@@ -419,6 +419,12 @@ Tile env_tile(bool *forced) {
     return Tile::T256x256;
 }
 
+// GEMMKIT_HIP_KSTREAM=0 keeps short contractions on the tile kernels.
+bool kstream_enabled() {
+    const char *s = getenv("GEMMKIT_HIP_KSTREAM");
+    return !(s && !strcmp(s, "0"));
+}
+
 // GEMMKIT_HIP_SKINNY=0 keeps products with a short side of 2..8 on the
 // wavefront-reduction GEMV instead of the matrix-core skinny kernel.
 bool skinny_enabled() {
@@ -928,10 +934,19 @@ int run_fit(const Region &rg, InType in, EpiParams ep, int64_t m, int64_t k, int
         }
         return finish("mfma gemm (split K)");
     }
-    double cost_whole = 0.0;
-    const Tile tile = pick_tile(M, N, batch, kbytes, ep.kind, in, &cost_whole);
     bool forced;
     env_tile(&forced);
+    // Short contractions are bound by the output write: the streaming kernel
+    // overlaps each tile's write with the next tile's loads (same results as
+    // the tile kernels, bit for bit).
+    if (!forced && kstream_enabled() && ep.kind != EpiKind::Q8 && kbytes <= kstream_max_kbytes() &&
+        M >= 128 && N >= 128) {
+        e = launch_kstream(in, args, ep, g_num_cus, tl_stream);
+        if (e != hipSuccess) return hip_fail(e, "kstream launch");
+        return finish("mfma gemm (short K)");
+    }
+    double cost_whole = 0.0;
+    const Tile tile = pick_tile(M, N, batch, kbytes, ep.kind, in, &cost_whole);
     TailSplit ts;
     if (!forced && batch == 1 && tail_split_enabled() &&
         plan_tail_split(M, N, kbytes, ep.kind, in, tile, cost_whole, &ts)) {

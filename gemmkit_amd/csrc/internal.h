@@ -84,6 +84,14 @@ hipError_t launch_mma_bf16(Tile tile, const MmaArgs &args, const EpiParams &ep, 
 hipError_t launch_mma(InType in, Tile tile, const MmaArgs &args, const EpiParams &ep,
                       hipStream_t stream);
 
+// Short-contraction route (kstream.hip): K*esz <= kstream_max_kbytes(), the
+// same kernel frame and bit-identical results as launch_mma, 128-row panels
+// streaming 128-column tiles with the output write overlapping the next
+// tile's loads.  Output kinds I32 (i8), F32 and BF16; no split K.
+int64_t kstream_max_kbytes();
+hipError_t launch_kstream(InType in, const MmaArgs &args, const EpiParams &ep, int cus,
+                          hipStream_t stream);
+
 // GEMV route (gemv.hip).  Dot form: out[r] = epi(sum_p mat[r,p] * vec_j[p]) for
 // nvec vectors (nvec <= 8); mat rows are k-contiguous.
 struct GemvArgs {

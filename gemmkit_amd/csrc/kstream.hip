@@ -1,0 +1,254 @@
+// kstream.hip -- matrix-core GEMM for a short contraction (K at most 256 bytes
+// per row: K <= 128 bf16, 64 f32, 256 i8), where the output write, not the
+// arithmetic, bounds the product: batched attention scores (64 x 512 x 512 x
+// 128 bf16 with f32 output write 67 MB and read 17 MB).
+//
+// Same kernel frame and arithmetic as mma_kernel (mma_kernel.h): C[M,N] =
+// epi(sum_k A[m,k] B[n,k]) with k-contiguous operands, the same MFMA
+// instructions fed the same 16-byte k chunks in the same order, so every
+// output is bit-identical to the tile kernels'.  What differs is the data
+// flow.  A workgroup owns a 128-row panel of one batch element and streams a
+// run of 128-column tiles across it:
+//   * one producer wave loads (direct-to-LDS) the panel's A rows once and
+//     the B rows of each tile into a two-slot ring, a tile ahead;
+//   * four consumer waves (2 x 2, 64 x 64 each) run the MFMAs of tile t from
+//     LDS, then write tile t through an LDS staging area as whole rows while
+//     the producer's loads of tile t+1 are in flight.
+// The consumer waves issue no loads, so their stores never hold up a wait
+// (loads and stores share one completion counter), and each workgroup writes
+// its tiles back to back instead of all 256 CUs writing at once at the end.
+// The whole contraction sits in LDS: rows are KB = 64, 128 or 256 bytes
+// (K*esz rounded up to a power of two; bytes past K load as zeros).
+#include "mma_kernel.h"
+
+namespace gk {
+
+constexpr int kKsTile = 128;                       // tile rows and columns
+constexpr int kKsConsumers = 4;                    // 2 x 2 waves of 64 x 64
+constexpr int kKsThreads = (kKsConsumers + 1) * 64;
+constexpr int kKsEpiLd = 64 + 4;                   // staging row stride (words)
+
+// Slot of 16-byte chunk c of row r in a KB-byte LDS row: 16 consecutive rows
+// reading one chunk hit 16 distinct 16-byte bank groups.
+template <int KB>
+__device__ __forceinline__ int ks_slot(int r, int c) {
+    constexpr int NCH = KB / 16;
+    return c ^ ((r / (16 / NCH)) & (NCH - 1));
+}
+
+template <InType T, EpiKind E, int KB>
+__global__ __launch_bounds__(kKsThreads) void kstream_kernel(const MmaArgs args, const EpiParams ep,
+                                                             int tiles_m, int tiles_n, int chunk,
+                                                             int nchunks) {
+    using M = Mma<T>;
+    using acc_t = typename M::acc_t;
+    using val_t = typename M::scalar_t;
+    constexpr int esz = (T == InType::I8) ? 1 : (T == InType::BF16 ? 2 : 4);
+    constexpr int TILE = kKsTile * KB;              // bytes of one 128-row operand tile
+    constexpr int NLD = TILE / 1024;                // 1 KiB loads per tile
+    constexpr int RPL = 1024 / KB;                  // rows one load fills
+    constexpr int CPR = KB / 16;                    // chunks per row
+    constexpr int SUB = KB / 32;                    // MFMA sub-steps
+    constexpr int STG = 32 * kKsEpiLd * 4;          // staging bytes per consumer wave
+    static_assert(NLD <= 32, "a tile's loads must fit the producer's load counter twice over");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[3 * TILE + kKsConsumers * STG];
+    uint8_t *const a_lds = smem;
+    uint8_t *const b_lds = smem + TILE;             // two slots of TILE bytes
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    // Unit -> (batch element, row panel, column chunk), XCD-contiguous so the
+    // panels of one element share an XCD's L2.
+    const int64_t unit = xcd_logical(blockIdx.x, gridDim.x);
+    const int64_t per_elem = (int64_t)tiles_m * nchunks;
+    const int64_t zb = unit / per_elem;
+    const int pm = (int)((unit % per_elem) / nchunks);
+    const int ch0 = (int)(unit % nchunks) * chunk;
+    const int ntile = tiles_n - ch0 < chunk ? tiles_n - ch0 : chunk;
+    const int m0 = pm * kKsTile;
+
+    const int64_t kbytes = (int64_t)args.K * esz;
+    // A row's bytes rounded up to whole chunks: a K*esz that is not a
+    // multiple of 16 only arrives through the pack, which zero-fills the rest
+    // of the chunk.
+    const int64_t kb16 = (kbytes + 15) / 16 * 16;
+    const int64_t lda_b = args.lda * esz, ldb_b = args.ldb * esz;
+    const uint8_t *A = (const uint8_t *)args.a + zb * args.bsa * esz + (int64_t)m0 * lda_b;
+    const uint8_t *B = (const uint8_t *)args.b + zb * args.bsb * esz;
+
+    if (wave == kKsConsumers) {
+        // ---------------------------------------------------------- producer
+        // Load q of a tile fills LDS bytes [q*1024, +1024): rows q*RPL + l/CPR,
+        // slot l%CPR holding chunk slot ^ swz(row); chunks at or past K read
+        // zeros (offset past the resource), as do rows past the matrix edge.
+        const int rl = lane / CPR, sl = lane % CPR;
+        auto load_tile = [&](const uint8_t *base, int64_t ld_b, int rows_valid, uint8_t *dst) {
+            const uint32_t num = rows_valid > 0 ? (uint32_t)((rows_valid - 1) * ld_b + kb16) : 0;
+#pragma unroll
+            for (int q = 0; q < NLD; ++q) {
+                const int row = q * RPL + rl;
+                const int c = ks_slot<KB>(row, sl);  // the swizzle is its own inverse
+                const bool in = (int64_t)c * 16 < kbytes && row < rows_valid;
+                const uint32_t off = in ? (uint32_t)(row * ld_b + c * 16) : kOutOfRange;
+                dma16(base, num, off, dst + q * 1024);
+            }
+        };
+        const int rows_a = args.M - m0 < kKsTile ? args.M - m0 : kKsTile;
+        load_tile(A, lda_b, rows_a, a_lds);
+        for (int t = 0; t < ntile; ++t) {
+            const int n0 = (ch0 + t) * kKsTile;
+            const int rows_b = args.N - n0 < kKsTile ? args.N - n0 : kKsTile;
+            load_tile(B + (int64_t)n0 * ldb_b, ldb_b, rows_b, b_lds + (t & 1) * TILE);
+            wait_vmcnt<0>();
+            stage_barrier();  // tile t's B (and the panel) landed; slot (t+1)&1 is free
+        }
+        stage_barrier();      // the consumers' last tile
+        return;
+    }
+
+    // ------------------------------------------------------------- consumers
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lrow = lane & 31, lhalf = lane >> 5;
+    int a_off[2], b_off[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) a_off[i] = (wm * 64 + i * 32 + lrow) * KB;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) b_off[j] = (wn * 64 + j * 32 + lrow) * KB;
+    val_t *const stg = (val_t *)(smem + 3 * TILE + wave * STG);
+    constexpr int CPRE = 16;              // 4-column chunks per staged row (64 columns)
+    constexpr int RPIT = 64 / CPRE;       // rows per read iteration
+    constexpr bool FB = E == EpiKind::F32 || E == EpiKind::BF16;
+
+    for (int t = 0; t < ntile; ++t) {
+        stage_barrier();  // tile t's B landed (and, for t > 0, the previous tile is done)
+        const uint8_t *bs = b_lds + (t & 1) * TILE;
+        acc_t acc[2][2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[i][j] = acc_t{};
+#pragma unroll
+        for (int s = 0; s < SUB; ++s) {
+            // (block bases are multiples of 32 rows, so the swizzle of row
+            // base + lrow is that of lrow)
+            const int slot = ks_slot<KB>(lrow, 2 * s + lhalf) << 4;
+            v4i af[2], bf[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) af[i] = *(const v4i *)(a_lds + a_off[i] + slot);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) bf[j] = *(const v4i *)(bs + b_off[j] + slot);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = M::step(bf[j], af[i], acc[i][j]);
+        }
+        // Epilogue through this wave's staging rows (32 at a time): register
+        // 4g+e of lane l is C row l%32, column 8g + 4*(l/32) + e of a block.
+        const int n0 = (ch0 + t) * kKsTile;
+        const int gcol0 = n0 + wn * 64;
+        float col_f[4] = {0, 0, 0, 0};
+        if constexpr (FB) {
+            if (ep.fused && ep.axis) {
+                const int cf = gcol0 + (lane % CPRE) * 4;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    col_f[e] = cf + e < args.N ? fused_bias<E == EpiKind::BF16>(ep, cf + e) : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            typedef val_t v4_t __attribute__((ext_vector_type(4)));
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const v4_t w = {(val_t)acc[i][j][4 * g], (val_t)acc[i][j][4 * g + 1],
+                                    (val_t)acc[i][j][4 * g + 2], (val_t)acc[i][j][4 * g + 3]};
+                    *(v4_t *)(stg + lrow * kKsEpiLd + j * 32 + 8 * g + 4 * lhalf) = w;
+                }
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): staging writes done
+            __builtin_amdgcn_wave_barrier();
+            const int grow0 = m0 + wm * 64 + i * 32;
+#pragma unroll
+            for (int it = 0; it < 32 / RPIT; ++it) {
+                const int row = it * RPIT + lane / CPRE;
+                const int c4 = (lane % CPRE) * 4;
+                const v4_t v4 = *(const v4_t *)(stg + row * kKsEpiLd + c4);
+                const val_t v[4] = {v4[0], v4[1], v4[2], v4[3]};
+                const int grow = grow0 + row;
+                float f4[4] = {col_f[0], col_f[1], col_f[2], col_f[3]};
+                if constexpr (FB) {
+                    if (ep.fused && !ep.axis) {
+                        const float f = grow < args.M ? fused_bias<E == EpiKind::BF16>(ep, grow) : 0.0f;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) f4[e] = f;
+                    }
+                }
+                if (grow < args.M && gcol0 + c4 < args.N)
+                    store4<E, val_t>(ep, zb, grow, gcol0 + c4, args.N, v, nullptr, nullptr, f4);
+            }
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // staging reads done before the next block
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+    stage_barrier();  // pairs with the producer's last barrier
+}
+
+// Column tiles per workgroup: all of a panel's when the panels alone give
+// every CU one, else the fewest that do.
+static int ks_chunk(int64_t panels, int tiles_n, int cus) {
+    if (panels >= cus) return tiles_n;
+    const int64_t split = (cus + panels - 1) / panels;
+    const int64_t s = split < tiles_n ? split : tiles_n;
+    return (int)((tiles_n + s - 1) / s);
+}
+
+template <InType T, EpiKind E, int KB>
+static hipError_t ks_go(const MmaArgs &args, const EpiParams &ep, int cus, hipStream_t stream) {
+    const int tiles_m = (args.M + kKsTile - 1) / kKsTile;
+    const int tiles_n = (args.N + kKsTile - 1) / kKsTile;
+    const int64_t panels = (int64_t)tiles_m * args.batch;
+    const int chunk = ks_chunk(panels, tiles_n, cus);
+    const int nchunks = (tiles_n + chunk - 1) / chunk;
+    const int64_t units = panels * nchunks;
+    if (units > INT32_MAX) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((kstream_kernel<T, E, KB>), dim3((unsigned)units), dim3(kKsThreads), 0,
+                       stream, args, ep, tiles_m, tiles_n, chunk, nchunks);
+    return hipGetLastError();
+}
+
+template <InType T, EpiKind E>
+static hipError_t ks_kb(const MmaArgs &args, const EpiParams &ep, int cus, hipStream_t stream) {
+    constexpr int esz = (T == InType::I8) ? 1 : (T == InType::BF16 ? 2 : 4);
+    const int64_t kb = (int64_t)args.K * esz;
+    if (kb <= 64) return ks_go<T, E, 64>(args, ep, cus, stream);
+    if (kb <= 128) return ks_go<T, E, 128>(args, ep, cus, stream);
+    return ks_go<T, E, 256>(args, ep, cus, stream);
+}
+
+int64_t kstream_max_kbytes() { return 256; }
+
+hipError_t launch_kstream(InType in, const MmaArgs &args, const EpiParams &ep, int cus,
+                          hipStream_t stream) {
+    // Tile rows are addressed as unsigned 32-bit offsets from the tile's
+    // first row: row strides must be non-negative and short enough.
+    if (args.lda < 0 || args.ldb < 0 || args.splits > 1 || args.batch < 1 ||
+        args.batch > kMaxGridZ || (int64_t)args.K * in_size(in) > kstream_max_kbytes())
+        return hipErrorInvalidValue;
+    switch (in) {
+    case InType::I8:
+        if (ep.kind == EpiKind::I32) return ks_kb<InType::I8, EpiKind::I32>(args, ep, cus, stream);
+        break;
+    case InType::BF16:
+        if (ep.kind == EpiKind::F32) return ks_kb<InType::BF16, EpiKind::F32>(args, ep, cus, stream);
+        if (ep.kind == EpiKind::BF16) return ks_kb<InType::BF16, EpiKind::BF16>(args, ep, cus, stream);
+        break;
+    case InType::F32:
+        if (ep.kind == EpiKind::F32) return ks_kb<InType::F32, EpiKind::F32>(args, ep, cus, stream);
+        break;
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace gk
