@@ -10,10 +10,12 @@
 // flow.  A workgroup owns a 128-row panel of one batch element and streams a
 // run of 128-column tiles across it:
 //   * one producer wave loads (direct-to-LDS) the panel's A rows once and
-//     the B rows of each tile into a two-slot ring, a tile ahead;
+//     the B rows of each tile into a ring of S slots (3 for 256-byte rows, 4
+//     for shorter ones), up to S tiles ahead: a tile's loads take a memory
+//     round trip, longer than the consumers spend on a tile;
 //   * four consumer waves (2 x 2, 64 x 64 each) run the MFMAs of tile t from
-//     LDS, then write tile t through an LDS staging area as whole rows while
-//     the producer's loads of tile t+1 are in flight.
+//     LDS, then write tile t through an LDS staging area (one 32 x 32 block at
+//     a time, as whole 128-byte row segments) while later tiles load.
 // The consumer waves issue no loads, so their stores never hold up a wait
 // (loads and stores share one completion counter), and each workgroup writes
 // its tiles back to back instead of all 256 CUs writing at once at the end.
@@ -26,7 +28,13 @@ namespace gk {
 constexpr int kKsTile = 128;                       // tile rows and columns
 constexpr int kKsConsumers = 4;                    // 2 x 2 waves of 64 x 64
 constexpr int kKsThreads = (kKsConsumers + 1) * 64;
-constexpr int kKsEpiLd = 64 + 4;                   // staging row stride (words)
+constexpr int kKsEpiLd = 32 + 4;                   // staging row stride (words)
+
+// B slots of the ring: as many as fit beside the panel and the staging.
+template <int KB>
+constexpr int ks_slots() {
+    return KB >= 256 ? 3 : 4;
+}
 
 // Slot of 16-byte chunk c of row r in a KB-byte LDS row: 16 consecutive rows
 // reading one chunk hit 16 distinct 16-byte bank groups.
@@ -50,10 +58,11 @@ __global__ __launch_bounds__(kKsThreads) void kstream_kernel(const MmaArgs args,
     constexpr int CPR = KB / 16;                    // chunks per row
     constexpr int SUB = KB / 32;                    // MFMA sub-steps
     constexpr int STG = 32 * kKsEpiLd * 4;          // staging bytes per consumer wave
-    static_assert(NLD <= 32, "a tile's loads must fit the producer's load counter twice over");
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[3 * TILE + kKsConsumers * STG];
+    constexpr int S = ks_slots<KB>();
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[(1 + S) * TILE + kKsConsumers * STG];
+    static_assert(sizeof(smem) <= 160 * 1024, "LDS");
     uint8_t *const a_lds = smem;
-    uint8_t *const b_lds = smem + TILE;             // two slots of TILE bytes
+    uint8_t *const b_lds = smem + TILE;             // S slots of TILE bytes
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -94,14 +103,30 @@ __global__ __launch_bounds__(kKsThreads) void kstream_kernel(const MmaArgs args,
                 dma16(base, num, off, dst + q * 1024);
             }
         };
-        const int rows_a = args.M - m0 < kKsTile ? args.M - m0 : kKsTile;
-        load_tile(A, lda_b, rows_a, a_lds);
-        for (int t = 0; t < ntile; ++t) {
+        auto load_b = [&](int t) {
             const int n0 = (ch0 + t) * kKsTile;
             const int rows_b = args.N - n0 < kKsTile ? args.N - n0 : kKsTile;
-            load_tile(B + (int64_t)n0 * ldb_b, ldb_b, rows_b, b_lds + (t & 1) * TILE);
-            wait_vmcnt<0>();
-            stage_barrier();  // tile t's B (and the panel) landed; slot (t+1)&1 is free
+            load_tile(B + (int64_t)n0 * ldb_b, ldb_b, rows_b, b_lds + (t % S) * TILE);
+        };
+        const int rows_a = args.M - m0 < kKsTile ? args.M - m0 : kKsTile;
+        load_tile(A, lda_b, rows_a, a_lds);
+        for (int t = 0; t < S && t < ntile; ++t) load_b(t);
+        // Tile t is waited for with the loads issued after it still in flight
+        // (loads complete in order; the counter holds at most 63, and waiting
+        // for that many or fewer is only stronger).  Barrier t publishes it;
+        // every consumer has then finished tile t-1, so its slot takes tile
+        // t-1+S.
+        int hi = (S < ntile ? S : ntile) - 1;  // last tile issued
+        for (int t = 0; t < ntile; ++t) {
+            const int after = hi - t;
+            if (after >= 2) wait_vmcnt<(2 * NLD < 63 ? 2 * NLD : 63)>();
+            else if (after == 1) wait_vmcnt<NLD>();
+            else wait_vmcnt<0>();
+            stage_barrier();
+            if (t >= 1 && t - 1 + S < ntile) {
+                load_b(t - 1 + S);
+                hi = t - 1 + S;
+            }
         }
         stage_barrier();      // the consumers' last tile
         return;
@@ -115,14 +140,14 @@ __global__ __launch_bounds__(kKsThreads) void kstream_kernel(const MmaArgs args,
     for (int i = 0; i < 2; ++i) a_off[i] = (wm * 64 + i * 32 + lrow) * KB;
 #pragma unroll
     for (int j = 0; j < 2; ++j) b_off[j] = (wn * 64 + j * 32 + lrow) * KB;
-    val_t *const stg = (val_t *)(smem + 3 * TILE + wave * STG);
-    constexpr int CPRE = 16;              // 4-column chunks per staged row (64 columns)
+    val_t *const stg = (val_t *)(smem + (1 + S) * TILE + wave * STG);
+    constexpr int CPRE = 8;               // 4-column chunks per staged row (32 columns)
     constexpr int RPIT = 64 / CPRE;       // rows per read iteration
     constexpr bool FB = E == EpiKind::F32 || E == EpiKind::BF16;
 
     for (int t = 0; t < ntile; ++t) {
         stage_barrier();  // tile t's B landed (and, for t > 0, the previous tile is done)
-        const uint8_t *bs = b_lds + (t & 1) * TILE;
+        const uint8_t *bs = b_lds + (t % S) * TILE;
         acc_t acc[2][2];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
@@ -143,53 +168,57 @@ __global__ __launch_bounds__(kKsThreads) void kstream_kernel(const MmaArgs args,
 #pragma unroll
                 for (int j = 0; j < 2; ++j) acc[i][j] = M::step(bf[j], af[i], acc[i][j]);
         }
-        // Epilogue through this wave's staging rows (32 at a time): register
-        // 4g+e of lane l is C row l%32, column 8g + 4*(l/32) + e of a block.
+        // Epilogue, one 32 x 32 block at a time through this wave's staging
+        // rows: register 4g+e of lane l is C row l%32, column 8g + 4*(l/32) + e
+        // of the block; rows come back as 128-byte segments (8 lanes a row).
         const int n0 = (ch0 + t) * kKsTile;
-        const int gcol0 = n0 + wn * 64;
-        float col_f[4] = {0, 0, 0, 0};
-        if constexpr (FB) {
-            if (ep.fused && ep.axis) {
-                const int cf = gcol0 + (lane % CPRE) * 4;
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    col_f[e] = cf + e < args.N ? fused_bias<E == EpiKind::BF16>(ep, cf + e) : 0.0f;
+        for (int j = 0; j < 2; ++j) {
+            const int gcol0 = n0 + wn * 64 + j * 32;
+            const int c4 = (lane % CPRE) * 4;
+            float col_f[4] = {0, 0, 0, 0};
+            if constexpr (FB) {
+                if (ep.fused && ep.axis) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        col_f[e] = gcol0 + c4 + e < args.N
+                                       ? fused_bias<E == EpiKind::BF16>(ep, gcol0 + c4 + e)
+                                       : 0.0f;
+                }
             }
-        }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            typedef val_t v4_t __attribute__((ext_vector_type(4)));
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int i = 0; i < 2; ++i) {
+                typedef val_t v4_t __attribute__((ext_vector_type(4)));
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const v4_t w = {(val_t)acc[i][j][4 * g], (val_t)acc[i][j][4 * g + 1],
                                     (val_t)acc[i][j][4 * g + 2], (val_t)acc[i][j][4 * g + 3]};
-                    *(v4_t *)(stg + lrow * kKsEpiLd + j * 32 + 8 * g + 4 * lhalf) = w;
+                    *(v4_t *)(stg + lrow * kKsEpiLd + 8 * g + 4 * lhalf) = w;
                 }
-            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): staging writes done
-            __builtin_amdgcn_wave_barrier();
-            const int grow0 = m0 + wm * 64 + i * 32;
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): staging writes done
+                __builtin_amdgcn_wave_barrier();
+                const int grow0 = m0 + wm * 64 + i * 32;
 #pragma unroll
-            for (int it = 0; it < 32 / RPIT; ++it) {
-                const int row = it * RPIT + lane / CPRE;
-                const int c4 = (lane % CPRE) * 4;
-                const v4_t v4 = *(const v4_t *)(stg + row * kKsEpiLd + c4);
-                const val_t v[4] = {v4[0], v4[1], v4[2], v4[3]};
-                const int grow = grow0 + row;
-                float f4[4] = {col_f[0], col_f[1], col_f[2], col_f[3]};
-                if constexpr (FB) {
-                    if (ep.fused && !ep.axis) {
-                        const float f = grow < args.M ? fused_bias<E == EpiKind::BF16>(ep, grow) : 0.0f;
+                for (int it = 0; it < 32 / RPIT; ++it) {
+                    const int row = it * RPIT + lane / CPRE;
+                    const v4_t v4 = *(const v4_t *)(stg + row * kKsEpiLd + c4);
+                    const val_t v[4] = {v4[0], v4[1], v4[2], v4[3]};
+                    const int grow = grow0 + row;
+                    float f4[4] = {col_f[0], col_f[1], col_f[2], col_f[3]};
+                    if constexpr (FB) {
+                        if (ep.fused && !ep.axis) {
+                            const float f =
+                                grow < args.M ? fused_bias<E == EpiKind::BF16>(ep, grow) : 0.0f;
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) f4[e] = f;
+                            for (int e = 0; e < 4; ++e) f4[e] = f;
+                        }
                     }
+                    if (grow < args.M && gcol0 + c4 < args.N)
+                        store4<E, val_t>(ep, zb, grow, gcol0 + c4, args.N, v, nullptr, nullptr, f4);
                 }
-                if (grow < args.M && gcol0 + c4 < args.N)
-                    store4<E, val_t>(ep, zb, grow, gcol0 + c4, args.N, v, nullptr, nullptr, f4);
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // staging reads done before the next block
+                __builtin_amdgcn_wave_barrier();
             }
-            __builtin_amdgcn_s_waitcnt(0xC07F);  // staging reads done before the next block
-            __builtin_amdgcn_wave_barrier();
         }
     }
     stage_barrier();  // pairs with the producer's last barrier
