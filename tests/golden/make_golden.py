@@ -19,6 +19,15 @@ own tests:
   tests/correctness/int8.rs:27.
 * kats.json -- literal known answers copied from the reference's tests
   (README 2x2, requant ties, the i8 wrap case).
+* generators.json -- the seeded streams the tests and the benchmark draw their
+  inputs from, restated in Python from the reference's definitions: Rng, the
+  xorshift* of tests/epilogue/common.rs:16-34 (next_u64, unit), with the i8
+  fills built on it (full range: next % 256 - 128; make_i8 of
+  tests/epilogue/requant.rs:25-30: next % 255 - 127); rand_vec of
+  tests/oracle_common/mod.rs:121-132 (xorshift64 13/7/17 from seed + the
+  golden-ratio constant, 2u - 1); and the Box-Muller normals over the Rng
+  stream (this build's own, u1 = (next >> 11 + 1) / 2^53, u2 = (next >> 11) /
+  2^53, r = sqrt(-2 ln u1), then r cos(2 pi u2) and r sin(2 pi u2)).
 
 Run: python tests/golden/make_golden.py
 """
@@ -102,6 +111,65 @@ def i8_small():
     return out
 
 
+class Rng:
+    """xorshift* of tests/epilogue/common.rs:16-34."""
+
+    def __init__(self, seed: int):
+        self.s = (seed | 1) & M64
+
+    def next_u64(self) -> int:
+        x = self.s
+        x ^= x >> 12
+        x ^= (x << 25) & M64
+        x ^= x >> 27
+        self.s = x
+        return (x * 0x2545F4914F6CDD1D) & M64
+
+    def unit(self) -> float:
+        return (self.next_u64() >> 11) / float(1 << 53) * 2.0 - 1.0
+
+
+def rand_vec(n: int, seed: int):
+    s = (seed + 0x9E3779B97F4A7C15) & M64
+    out = []
+    for _ in range(n):
+        s ^= (s << 13) & M64
+        s ^= s >> 7
+        s ^= (s << 17) & M64
+        out.append(2.0 * ((s >> 11) / float(1 << 53)) - 1.0)
+    return out
+
+
+def normals(n: int, seed: int):
+    import math
+    r_ = Rng(seed)
+    out = []
+    while len(out) < n:
+        u1 = ((r_.next_u64() >> 11) + 1.0) / float(1 << 53)
+        u2 = (r_.next_u64() >> 11) / float(1 << 53)
+        r = math.sqrt(-2.0 * math.log(u1))
+        out.append(r * math.cos(2 * math.pi * u2))
+        out.append(r * math.sin(2 * math.pi * u2))
+    return out[:n]
+
+
+def generators():
+    out = {"next_u64": {}, "i8_full": {}, "i8_sym127": {}, "unit": {}, "rand_vec": {},
+           "normal": {}}
+    for seed in (0, 1, 2, 7, 0x123456789ABCDEF, 2**64 - 2):
+        r = Rng(seed)
+        out["next_u64"][str(seed)] = [r.next_u64() for _ in range(64)]
+        r = Rng(seed)
+        out["i8_full"][str(seed)] = [r.next_u64() % 256 - 128 for _ in range(300)]
+        r = Rng(seed)
+        out["i8_sym127"][str(seed)] = [r.next_u64() % 255 - 127 for _ in range(300)]
+        r = Rng(seed)
+        out["unit"][str(seed)] = [r.unit().hex() for _ in range(64)]
+        out["rand_vec"][str(seed)] = [v.hex() for v in rand_vec(64, seed)]
+        out["normal"][str(seed)] = [v.hex() for v in normals(63, seed)]
+    return out
+
+
 def kats():
     return {
         # README.md:55-71, src/lib.rs:9-25
@@ -123,6 +191,8 @@ def main():
         json.dump(i8_small(), f, separators=(",", ":"))
     with open(os.path.join(HERE, "kats.json"), "w") as f:
         json.dump(kats(), f, indent=1)
+    with open(os.path.join(HERE, "generators.json"), "w") as f:
+        json.dump(generators(), f, separators=(",", ":"))
 
 
 if __name__ == "__main__":

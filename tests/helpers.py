@@ -41,3 +41,17 @@ def to_dev(x: np.ndarray, dev) -> torch.Tensor:
 
 def bf16_tensor_from_bits(bits: np.ndarray, dev) -> torch.Tensor:
     return torch.from_numpy(bits.view(np.int16).copy()).to(dev).view(torch.bfloat16)
+
+
+def rel_errors(got: np.ndarray, ref: np.ndarray, floor_frac: float = 1e-3):
+    """(floored, unfloored) maximum relative error of got against ref: the
+    floored one divides by max(|ref|, floor_frac * max|ref|), the unfloored one
+    by |ref| over the elements where ref != 0."""
+    got = np.asarray(got, np.float64).ravel()
+    ref = np.asarray(ref, np.float64).ravel()
+    err = np.abs(got - ref)
+    floor = floor_frac * np.abs(ref).max()
+    floored = float((err / np.maximum(np.abs(ref), floor)).max())
+    nz = ref != 0
+    unfloored = float((err[nz] / np.abs(ref[nz])).max()) if nz.any() else 0.0
+    return floored, unfloored

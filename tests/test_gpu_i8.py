@@ -116,8 +116,11 @@ def test_degenerate_k0_and_alpha0(dev):
 
 
 def test_4096_cube_benchmark_shape(dev):
-    """The benchmark workload: sampled rows exact vs the oracle, plus the exact
-    checksum sum_i C[i, j] == sum_p (sum_i A[i, p]) B[p, j] for every column."""
+    """The benchmark workload, every element: against the CPU port of gemmkit's
+    i8 path (oracle/cpu_port.c, itself pinned bit-exact to the oracle's closed
+    form in test_oracle.py), plus sampled rows against the closed form directly
+    and the exact checksum sum_i C[i, j] == sum_p (sum_i A[i, p]) B[p, j] for
+    every column."""
     import torch
     M = K = N = 4096
     a = oracle.rng_i8_full(1, M * K)
@@ -135,6 +138,10 @@ def test_4096_cube_benchmark_shape(dev):
     colsum = oracle.colsum_i32(M, N, got, N, 1)
     abft = oracle.abft_i8(M, K, N, a, K, 1, b, 1, K)
     assert np.array_equal(colsum, abft)
+    full = np.empty(M * N, np.int32)
+    oracle.port_gemm_i8(M, K, N, 1, a, K, 1, b, 1, K, 0, full, N, 1)
+    bad = np.flatnonzero(got != full)
+    assert bad.size == 0, f"{bad.size} of {M * N} elements differ, first at {bad[:5]}"
 
 
 @pytest.mark.parametrize("m,k,n", [(300, 64, 200), (5, 96, 300), (300, 128, 9)])

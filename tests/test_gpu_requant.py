@@ -164,9 +164,13 @@ def test_packed_requant_matches_plain(dev, u8):
 def test_linear_layer_full_size(dev):
     """The int8 linear layer at full size: Y (2048 x 11008, token-major) =
     requant(X (2048 x 4096) . W^T), W prepacked once and reused, per-output-channel
-    scale and bias, zp 0, ReLU.  Every output byte is checked: the i32 GEMM of the
-    same operands (checked by sampled rows and the exact column checksum) mapped
-    through the oracle's requant map must equal the fused result, on two calls."""
+    scale and bias, zp 0, ReLU.  Every element is checked against the CPU port
+    of gemmkit's paths (oracle/cpu_port.c, pinned bit-exact to the oracle's
+    closed forms in test_oracle.py): the i32 GEMM of the same operands against
+    the port's i32 GEMM (and sampled rows against the closed form, plus the
+    exact column checksum), and the fused bytes, on two calls, against the
+    port's requantizing path on a prepacked W and against the oracle's requant
+    map of the port's i32."""
     import torch
     T, K, Nc = 2048, 4096, 11008
     x = oracle.rng_i8_sym127(21, T * K)
@@ -186,8 +190,16 @@ def test_linear_layer_full_size(dev):
         assert np.array_equal(acc_h[r * Nc:(r + 1) * Nc], row), f"row {r}"
     assert np.array_equal(oracle.colsum_i32(T, Nc, acc_h, Nc, 1),
                           oracle.abft_i8(T, K, Nc, x, K, 1, w, 1, K))
+    acc_port = np.empty(T * Nc, np.int32)
+    oracle.port_gemm_i8(T, K, Nc, 1, x, K, 1, w, 1, K, 0, acc_port, Nc, 1)
+    assert np.array_equal(acc_h, acc_port)
     want = np.zeros(T * Nc, np.int8)
-    oracle.requant_map(T, Nc, acc_h, Nc, 1, 0.0, scale, 0, bias, 1, 0, 127, want, Nc, 1)
+    oracle.requant_map(T, Nc, acc_port, Nc, 1, 0.0, scale, 0, bias, 1, 0, 127, want, Nc, 1)
+    want_port = np.zeros(T * Nc, np.int8)
+    pb = oracle.PortPackedB(K, Nc, w, 1, K)
+    oracle.port_gemm_i8_requant(T, K, Nc, x, K, 1, None, 0, 0, 0.0, scale, 0, bias, 1, 0, 127,
+                                want_port.view(np.uint8), Nc, 1, packed=pb)
+    assert np.array_equal(want_port, want)
     packed = gk.prepack_rhs_i8(gk.MatRef(wd, K, Nc, 1, K))
     req = gk.Requantize(gk.RequantScale.PerCol(to_dev(scale, dev)), 0, to_dev(bias, dev),
                         bias_axis="col", relu=True)

@@ -404,3 +404,29 @@ def test_cpu_port_gemv_within_tolerance(rows, k, beta):
     got = y0.copy()
     oracle.port_gemv_f32(rows, k, 1.25, a, k, x, beta, got, 1, threads=3)
     assert _rel_frob(got, ref) <= 1e-5
+
+
+def test_generators_match_python_restatement():
+    """The oracle's seeded streams (the inputs of the parity tests and the
+    benchmark) against tests/golden/generators.json, written by a Python
+    restatement of the reference's Rng (tests/epilogue/common.rs:16-34) and
+    rand_vec (tests/oracle_common/mod.rs:121-132): integers exact, uniform
+    floats bit-exact, Box-Muller normals within 4 ulp (libm cos/sin/log)."""
+    path = os.path.join(os.path.dirname(__file__), "golden", "generators.json")
+    g = json.load(open(path))
+    for seed_s, want in g["next_u64"].items():
+        assert oracle.rng_next_u64(int(seed_s), len(want)) == want, seed_s
+    for seed_s, want in g["i8_full"].items():
+        assert oracle.rng_i8_full(int(seed_s), len(want)).tolist() == want, seed_s
+    for seed_s, want in g["i8_sym127"].items():
+        assert oracle.rng_i8_sym127(int(seed_s), len(want)).tolist() == want, seed_s
+    for seed_s, want in g["unit"].items():
+        got = oracle.rng_unit(int(seed_s), len(want))
+        assert [float.fromhex(w) for w in want] == got.tolist(), seed_s
+    for seed_s, want in g["rand_vec"].items():
+        got = oracle.rand_vec(int(seed_s), len(want))
+        assert [float.fromhex(w) for w in want] == got.tolist(), seed_s
+    for seed_s, want in g["normal"].items():
+        got = oracle.rng_normal(int(seed_s), len(want))
+        w = np.array([float.fromhex(x) for x in want])
+        assert np.allclose(got, w, rtol=4 * 2.0 ** -52, atol=4 * 2.0 ** -52), seed_s
