@@ -232,11 +232,12 @@ def test_bf16_out_narrowing_top_exponent_and_overflow(dev, m, n):
     sb = rng.choice([-1.0, 1.0], n)
     av = (sa * _mantissas(rng, m) * np.exp2(rng.integers(53, 56, m))).astype(np.float32)
     bv = (sb * _mantissas(rng, n) * np.exp2(rng.integers(52, 55, n))).astype(np.float32)
-    if m >= 3 and n >= 3:
-        # 73 * 7 = 511 = 0x1FF: 511 * 2^119 is 0x7F7F8000, the midpoint to inf
-        av[:3] = [73.0 * 2.0 ** 60, -73.0 * 2.0 ** 60, 127.0 * 2.0 ** 60]
-        # 255 * 2 = 510 = 0x1FE: 510 * 2^119 ... and 127*4+1 style neighbours
-        bv[:3] = [7.0 * 2.0 ** 40, 2.0 * 2.0 ** 40, 4.0 * 2.0 ** 40]
+    # 73 * 7 = 511 = 0x1FF: 511 * 2^119 is f32 0x7F7F8000, the midpoint to
+    # infinity (and its negative); 127 * 4 * 2^119 is the largest bf16 exactly
+    av[0] = 73.0 * 2.0 ** 60
+    bv[:3] = [7.0 * 2.0 ** 40, -7.0 * 2.0 ** 40, 4.0 * 2.0 ** 40][:n]
+    if m >= 3:
+        av[1:3] = [-73.0 * 2.0 ** 60, 127.0 * 2.0 ** 60]
     got, want, v = _narrow_case(dev, av, bv, 2.0 ** 19)
     top = np.abs(v) >= np.float32(2.0 ** 126)
     assert top.mean() > 0.3
