@@ -17,12 +17,18 @@
 //     chunks once into registers; the next row group's matrix loads are issued
 //     before the current group is multiplied, so one group is always in flight
 //     behind the arithmetic.
-//   * gemv_lds: longer rows.  The vectors are staged once per workgroup in LDS
-//     and each lane keeps UNROLL chunks per row in flight.
+//   * gemv_wgrow: longer rows, one or two vectors.  The vectors are staged
+//     once per workgroup in LDS and the whole workgroup reads one row at a
+//     time, 32 KiB per batch, the next batch in flight behind the current.
+//   * gemv_lds: longer rows, more vectors.  The vectors are staged in LDS and
+//     each lane keeps UNROLL chunks per row in flight.
 // Per-lane partial sums of the RPW x NV outputs of a row group are combined by
 // a butterfly over the 64 lanes that halves the number of values each lane
 // carries at every step (V values cost V-1 + log2(64/V) shuffles instead of
 // 6*V), leaving output v on lanes [v*64/V, (v+1)*64/V).
+#include <stdio.h>
+#include <stdlib.h>
+
 #include "epilogue.h"
 
 namespace gk {
@@ -268,6 +274,112 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_lds(const GemvArgs g, const
     }
 }
 
+// Long rows with one or two vectors: the workgroup takes one row at a time
+// (rows blockIdx.x, + gridDim.x, ...), its 256 lanes reading 256*U
+// consecutive 16-byte chunks per batch (thread t: chunks t + 256u), so each
+// workgroup streams one contiguous 32..64 KiB window instead of four waves
+// streaming four rows 8 KiB at a time (on a 16384^2 f32 matrix: 0.86 of HBM
+// peak for this access pattern against 0.82 for a row per wave and 0.77 for
+// two rows per wave, plain reads measured alone).  Batches run as one flat
+// sequence over the workgroup's rows with the next batch's loads issued
+// before the current one is multiplied; the last batch of a row is masked
+// past the row's end.  At a row's end each wave reduces its lanes'
+// partial sums, the four wave totals meet in LDS (two slots alternating by
+// row, so one barrier per row suffices) and wave 0 adds them in wave order
+// and stores.
+template <InType T, EpiKind E, int NV, int U>
+__global__ __launch_bounds__(kGemvThreads) void gemv_wgrow(const GemvArgs g, const EpiParams ep) {
+    using D = Dot16<T>;
+    using acc_t = typename D::acc_t;
+    extern __shared__ __attribute__((aligned(16))) uint8_t sv[];
+    constexpr int esz = (T == InType::I8) ? 1 : (T == InType::BF16 ? 2 : 4);
+    const int64_t nch = ((int64_t)g.K * esz + 15) / 16;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t zb = blockIdx.y;  // batch element
+    const uint8_t *vec = (const uint8_t *)g.vec + zb * g.bsv * esz;
+    const int64_t vld_b = g.vld * esz;
+    // The vectors are staged in LDS when they fit (else read from global
+    // memory, L2-resident); the wave-total exchange follows them.
+    const bool staged = (int64_t)NV * nch * 16 <= kGemvLdsMax;
+    acc_t *comb = (acc_t *)(sv + (staged ? NV * nch * 16 : 0));
+    if (staged) {
+        for (int64_t c = tid; c < NV * nch; c += kGemvThreads) {
+            const int64_t j = c / nch, ch = c % nch;
+            *(v4i_g *)(sv + c * 16) = j < g.nvec ? *(const v4i_g *)(vec + j * vld_b + ch * 16)
+                                                 : v4i_g{0, 0, 0, 0};
+        }
+    }
+    __syncthreads();
+    auto xchunk = [&](int j, int64_t ch) -> v4i_g {
+        if (staged) return *(const v4i_g *)(sv + (j * nch + ch) * 16);
+        return j < g.nvec ? *(const v4i_g *)(vec + j * vld_b + ch * 16) : v4i_g{0, 0, 0, 0};
+    };
+    const uint8_t *mat = (const uint8_t *)g.mat + zb * g.bsm * esz;
+    const int64_t ld_b = g.ld * esz;
+    constexpr int64_t kBatch = (int64_t)kGemvThreads * U;  // chunks per batch
+    const int64_t nbr = (nch + kBatch - 1) / kBatch;       // batches per row
+    int64_t irow = blockIdx.x, ib = 0;  // next batch to issue
+    int64_t rrow = blockIdx.x, rb = 0;  // next batch to multiply
+    int slot = 0;
+    acc_t acc[NV];
+    auto issue = [&](v4i_g (&m)[U]) {
+        const uint8_t *rp = mat + irow * ld_b;
+        const int64_t c0 = ib * kBatch + tid;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t c = c0 + (int64_t)kGemvThreads * u;
+            m[u] = c < nch ? __builtin_nontemporal_load((const v4i_g *)(rp + c * 16))
+                           : v4i_g{0, 0, 0, 0};
+        }
+        if (++ib == nbr) {
+            ib = 0;
+            irow += gridDim.x;
+        }
+    };
+    auto run = [&](const v4i_g (&m)[U]) {
+        if (rb == 0) {
+#pragma unroll
+            for (int j = 0; j < NV; ++j) acc[j] = acc_t(0);
+        }
+        const int64_t c0 = rb * kBatch + tid;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t c = c0 + (int64_t)kGemvThreads * u;
+            if (c < nch) {
+#pragma unroll
+                for (int j = 0; j < NV; ++j) acc[j] = D::dot(m[u], xchunk(j, c), acc[j]);
+            }
+        }
+        if (++rb < nbr) return;
+        acc_t v[NV];
+#pragma unroll
+        for (int j = 0; j < NV; ++j) v[j] = acc[j];
+        wave_reduce(v);
+        constexpr int SH = 6 - log2c<NV>();
+        if ((lane & ((1 << SH) - 1)) == 0)
+            comb[(slot * kGemvWaves + wave) * NV + (lane >> SH)] = v[0];
+        __syncthreads();
+        if (wave == 0 && lane < NV) {
+            acc_t s = comb[slot * kGemvWaves * NV + lane];
+#pragma unroll
+            for (int w = 1; w < kGemvWaves; ++w) s += comb[(slot * kGemvWaves + w) * NV + lane];
+            if (lane < g.nvec) Store<E>::apply(ep, blockIdx.y, lane, (int)rrow, s);
+        }
+        slot ^= 1;
+        rb = 0;
+        rrow += gridDim.x;
+    };
+    v4i_g m0[U], m1[U];
+    if (irow < g.R) issue(m0);
+    while (rrow < g.R) {
+        if (irow < g.R) issue(m1);
+        run(m0);
+        if (rrow >= g.R) break;
+        if (irow < g.R) issue(m0);
+        run(m1);
+    }
+}
+
 // Persistent grid: enough workgroups to cover the row groups, at most
 // `per_cu` per CU over all batch elements (grid y); every element gets at
 // least one workgroup.
@@ -297,18 +409,66 @@ constexpr int reg_per_cu() {
     return CPL >= 4 ? 3 : 8;
 }
 
+// GEMMKIT_HIP_GEMV_SHAPE="rows,wgs" overrides the register GEMV's launch shape:
+// rows per wave iteration (1, 2 or 4; one vector only) and workgroups per CU.
+// A tuning switch for the launch-shape sweep: i8 results do not change; float
+// sums may round differently with the rows per iteration (the butterfly's
+// tree depends on the number of values it reduces).
+struct GemvShape {
+    int rpw = 0, per_cu = 0;
+};
+static GemvShape gemv_shape_env() {
+    GemvShape sh;
+    const char *e = getenv("GEMMKIT_HIP_GEMV_SHAPE");
+    if (e && sscanf(e, "%d,%d", &sh.rpw, &sh.per_cu) != 2) sh = GemvShape{};
+    return sh;
+}
+
+template <InType T, EpiKind E, int NV, int CPL, int RPW>
+static hipError_t go_reg_rpw(const GemvArgs &g, const EpiParams &ep, int per_cu,
+                             hipStream_t stream) {
+    const int64_t groups = ((int64_t)g.R + RPW - 1) / RPW;
+    hipLaunchKernelGGL((gemv_reg<T, E, NV, CPL, RPW>), gemv_grid(groups, g.cus, per_cu, g.batch),
+                       dim3(kGemvThreads), 0, stream, g, ep);
+    return hipGetLastError();
+}
+
 template <InType T, EpiKind E, int NV, int CPL>
 static hipError_t go_reg(const GemvArgs &g, const EpiParams &ep, hipStream_t stream) {
-    constexpr int RPW = rows_per_wave<CPL>();
-    const int64_t groups = ((int64_t)g.R + RPW - 1) / RPW;
-    hipLaunchKernelGGL((gemv_reg<T, E, NV, CPL, RPW>), gemv_grid(groups, g.cus, reg_per_cu<CPL>(), g.batch),
-                       dim3(kGemvThreads), 0, stream, g, ep);
+    const GemvShape sh = gemv_shape_env();
+    const int per_cu = sh.per_cu > 0 ? sh.per_cu : reg_per_cu<CPL>();
+    if constexpr (NV == 1) {
+        if (sh.rpw == 1) return go_reg_rpw<T, E, NV, CPL, 1>(g, ep, per_cu, stream);
+        if (sh.rpw == 2) return go_reg_rpw<T, E, NV, CPL, 2>(g, ep, per_cu, stream);
+        if (sh.rpw == 4) return go_reg_rpw<T, E, NV, CPL, 4>(g, ep, per_cu, stream);
+    }
+    return go_reg_rpw<T, E, NV, CPL, rows_per_wave<CPL>()>(g, ep, per_cu, stream);
+}
+
+// Workgroup-per-row launch: as many workgroups per CU as LDS holds, at most
+// 3 (2 and 3 measure alike; 4 or more contend in HBM), or the switch's count.
+template <InType T, EpiKind E, int NV, int U>
+static hipError_t go_wgrow(const GemvArgs &g, const EpiParams &ep, hipStream_t stream) {
+    constexpr int esz = (T == InType::I8) ? 1 : (T == InType::BF16 ? 2 : 4);
+    const int64_t vbytes = (int64_t)NV * (((int64_t)g.K * esz + 15) / 16) * 16;
+    const size_t shm = (vbytes <= kGemvLdsMax ? (size_t)vbytes : 0) + 2 * kGemvWaves * NV * 4;
+    const int fit = (int)(160 * 1024 / shm);
+    int per_cu = fit < 3 ? (fit > 1 ? fit : 1) : 3;
+    const GemvShape sh = gemv_shape_env();
+    if (sh.per_cu > 0) per_cu = sh.per_cu < fit ? sh.per_cu : (fit > 1 ? fit : 1);
+    const int64_t nb = g.batch > 1 ? g.batch : 1;
+    int64_t blocks = ((int64_t)(g.cus > 0 ? g.cus : 256) * per_cu + nb - 1) / nb;
+    if (blocks > g.R) blocks = g.R;
+    hipLaunchKernelGGL((gemv_wgrow<T, E, NV, U>), dim3((unsigned)blocks, (unsigned)nb),
+                       dim3(kGemvThreads), shm, stream, g, ep);
     return hipGetLastError();
 }
 
 template <InType T, EpiKind E, int NV>
 static hipError_t go_lds(const GemvArgs &g, const EpiParams &ep, hipStream_t stream) {
-    constexpr int RPW = NV <= 2 ? 2 : 1;
+    // one or two vectors (bf16: one, for registers): a workgroup per row
+    if constexpr (T == InType::BF16 ? NV == 1 : NV <= 2) return go_wgrow<T, E, NV, 8>(g, ep, stream);
+    constexpr int RPW = 1;
     constexpr int esz = (T == InType::I8) ? 1 : (T == InType::BF16 ? 2 : 4);
     const int64_t vbytes = (int64_t)NV * (((int64_t)g.K * esz + 15) / 16) * 16;
     const size_t shm = vbytes <= kGemvLdsMax ? (size_t)vbytes : 0;

@@ -30,6 +30,9 @@
 // The vectors may have any strides: k-contiguous, 16-byte aligned rows are
 // staged as 16-byte chunks, anything else element by element (so a strided
 // activation needs no separate pack launch).
+#include <stdio.h>
+#include <stdlib.h>
+
 #include <type_traits>
 
 #include "epilogue.h"
@@ -320,19 +323,32 @@ static hipError_t skinny_go(const GemvArgs &g, const EpiParams &ep, hipStream_t 
     // 32-row items when there are enough of them for every CU, else 8-row
     // items (4x as many workgroups streaming the same bytes).
     const int64_t R = g.R;
-    const bool wide = (R + 31) / 32 >= cus;
-    const int64_t items = wide ? (R + 31) / 32 : (R + 7) / 8;
+    int rows = (R + 31) / 32 >= cus ? 32 : 8;
+    // GEMMKIT_HIP_SKINNY_SHAPE="rows,wgs": rows per work item (8, 16 or 32)
+    // and workgroups per CU, a tuning switch for the launch-shape sweep
+    // (results do not change: each row's K ranges and their order are fixed
+    // by K).
+    int rows_env = 0, wgs_env = 0;
+    if (const char *e = getenv("GEMMKIT_HIP_SKINNY_SHAPE"))
+        if (sscanf(e, "%d,%d", &rows_env, &wgs_env) == 2 &&
+            (rows_env == 8 || rows_env == 16 || rows_env == 32))
+            rows = rows_env;
+    const int64_t items = (R + rows - 1) / rows;
     // As many resident workgroups per CU as its 160 KiB of LDS holds (<= 4).
     const int fit = (int)(160 * 1024 / shm);
-    const int per_cu = fit < 4 ? (fit > 1 ? fit : 1) : 4;
+    int per_cu = fit < 4 ? (fit > 1 ? fit : 1) : 4;
+    if (wgs_env > 0) per_cu = wgs_env < fit ? wgs_env : (fit > 1 ? fit : 1);
     // Batch elements share the persistent grid (grid y), each at least one
     // workgroup.
     const int64_t nb = g.batch > 1 ? g.batch : 1;
     int64_t blocks = ((int64_t)cus * per_cu + nb - 1) / nb;
     if (blocks > items) blocks = items;
     const dim3 grid((unsigned)blocks, (unsigned)nb);
-    if (wide)
+    if (rows == 32)
         hipLaunchKernelGGL((skinny_mfma<T, E, 4>), grid, dim3(kSkThreads), (size_t)shm, stream, g,
+                           ep);
+    else if (rows == 16)
+        hipLaunchKernelGGL((skinny_mfma<T, E, 2>), grid, dim3(kSkThreads), (size_t)shm, stream, g,
                            ep);
     else
         hipLaunchKernelGGL((skinny_mfma<T, E, 1>), grid, dim3(kSkThreads), (size_t)shm, stream, g,

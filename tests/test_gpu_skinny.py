@@ -39,6 +39,9 @@ I8_CASES = [
     (100, 64, 1), (257, 48, 2), (1000, 4096, 7), (33, 1040, 12), (300, 4112, 16),
     # one vector, 1..8 KiB rows (4, 4, 2 and 1 rows per wave iteration), ragged row counts
     (1, 1024, 257), (1, 2048, 1001), (1, 4096, 3), (1, 8192, 301), (1001, 8192, 1),
+    # one vector, rows past 8 KiB (the streaming kernel): whole batches only, and a
+    # ragged last batch
+    (1, 16384, 513), (1, 20000, 300), (700, 20000, 1),
 ]
 
 
@@ -85,7 +88,9 @@ def test_decode_gemv_full_size(dev, m):
                                    # 2..4 vectors with 4..8 KiB rows: the wavefront GEMV
                                    (2, 1024, 700), (3, 2048, 301), (600, 1536, 4), (4, 2048, 64),
                                    # one vector, 4 and 8 KiB rows, ragged row counts
-                                   (1, 1024, 3), (1, 2048, 257), (513, 2048, 1)])
+                                   (1, 1024, 3), (1, 2048, 257), (513, 2048, 1),
+                                   # rows past 8 KiB, ragged last batch
+                                   (1, 16400, 129), (2, 9000, 77)])
 @pytest.mark.parametrize("alpha,beta", [(1.0, 0.0), (0.75, -1.5)])
 def test_f32_skinny(dev, m, k, n, alpha, beta):
     a = oracle.rand_vec(41 + m, m * k).astype(np.float32).reshape(m, k)
@@ -103,7 +108,8 @@ def test_f32_skinny(dev, m, k, n, alpha, beta):
     assert rel_frob(got, ref) <= 1e-5
 
 
-@pytest.mark.parametrize("m,k,n", [(1, 4096, 1000), (8, 2048, 333), (300, 512, 12)])
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 1000), (8, 2048, 333), (300, 512, 12),
+                                   (1, 12000, 300)])
 def test_bf16_f32out_skinny(dev, m, k, n):
     import torch
     g = torch.Generator().manual_seed(m * 1000 + n)
