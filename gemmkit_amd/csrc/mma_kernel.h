@@ -698,7 +698,7 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
                 }
             }
             if (grow < args.M && gcol0 + c4 < args.N)
-                store4<E, val_t>(ep, z, grow, gcol0 + c4, args.N, v, s4, b4, f4);
+                store4<E, val_t, false>(ep, z, grow, gcol0 + c4, args.N, v, s4, b4, f4);
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_wave_barrier();

@@ -97,15 +97,36 @@ inline int32_t requant_fast(int32_t acc, int32_t bias, float scale, int32_t zp, 
     return q;
 }
 
-// requant_fast without branches, for the device epilogue: the f32 path with
-// its tie correction as selects.  `slow` is set when this lane must take
-// requant_bits instead: an operand of 2^24 or more or a non-finite scale.
-// Callers check slow for the whole wave once per group of elements, so the
-// exceptional path costs nothing when no lane needs it.
+// The device epilogue's form of requant_fast, in three tiers so the common
+// case costs about a dozen VALU instructions per value:
+//   requant_f32      rint of the f32 product, clamp, zero point, band.  Exact
+//                    unless the f32 product sits on a half (`tie`: the sign
+//                    of the product's low part may then decide) or the lane
+//                    needs the integer path (`slow`: |acc + bias| >= 2^24,
+//                    where the f32 operand is no longer exact, or a
+//                    non-finite product -- a NaN or infinite scale, or an f32
+//                    overflow);
+//   requant_f32_tie  the same with the two-float tie correction (exact for
+//                    every lane that is not slow);
+//   requant_bits     exact for every input.
+// Callers evaluate requant_f32 and take a later tier for the whole wave only
+// when some lane flags it, so the exceptional paths cost nothing when no lane
+// needs them.
 struct RequantF32 {
     int32_t q;
     bool slow;
+    bool tie;
 };
+
+inline int32_t requant_band(float t, int32_t zp, int32_t lo, int32_t hi) {
+    // Anything beyond 2^24 (|zp| <= 255) lands on a band edge: clamp before
+    // converting.
+    t = __builtin_fminf(__builtin_fmaxf(t, -16777216.0f), 16777216.0f);
+    int32_t q = (int32_t)t + zp;
+    q = q < lo ? lo : q;
+    q = q > hi ? hi : q;
+    return q;
+}
 
 inline RequantF32 requant_f32(int32_t acc, int32_t bias, float scale, int32_t zp, int32_t lo,
                                  int32_t hi) {
@@ -113,21 +134,29 @@ inline RequantF32 requant_f32(int32_t acc, int32_t bias, float scale, int32_t zp
     const int32_t v = (int32_t)((uint32_t)acc + (uint32_t)bias);
     const float vf = (float)v;
     const float ph = vf * scale;
-    const float pl = __builtin_fmaf(vf, scale, -ph);
-    // rint by the 1.5 * 2^23 shift: exact round-half-to-even for |ph| < 2^22;
-    // larger products land beyond the band and saturate either way.
-    constexpr float kShift = 12582912.0f;
-    float t = (ph + kShift) - kShift;
+    const float t = __builtin_rintf(ph);
+    RequantF32 r;
+    r.tie = __builtin_fabsf(ph - t) == 0.5f;
+    r.slow = !(__builtin_fabsf(vf) < 16777216.0f) || !(__builtin_fabsf(ph) < __builtin_inff());
+    r.q = requant_band(t, zp, lo, hi);
+    return r;
+}
+
+inline int32_t requant_f32_tie(int32_t acc, int32_t bias, float scale, int32_t zp, int32_t lo,
+                                  int32_t hi) {
+#pragma clang fp contract(off)
+    const int32_t v = (int32_t)((uint32_t)acc + (uint32_t)bias);
+    const float vf = (float)v;
+    const float ph = vf * scale;
+    const float pl = __builtin_fmaf(vf, scale, -ph);  // ph + pl = the exact product
+    float t = __builtin_rintf(ph);
     const float d = ph - t;
-    // hi + lo on a half: the sign of lo decides (see requant_fast)
-    t += (d == 0.5f && pl > 0.0f) ? 1.0f : ((d == -0.5f && pl < 0.0f) ? -1.0f : 0.0f);
-    const bool slow = (uint32_t)v + (1u << 24) >= (1u << 25) ||
-                      (__builtin_bit_cast(uint32_t, scale) & 0x7F800000u) == 0x7F800000u;
-    t = __builtin_fminf(__builtin_fmaxf(t, -16777216.0f), 16777216.0f);
-    int32_t q = (int32_t)t + zp;
-    q = q < lo ? lo : q;
-    q = q > hi ? hi : q;
-    return RequantF32{q, slow};
+    // On a half, rint chose the even neighbour; the exact product lies past
+    // the half (away from t) when pl has the sign of d.  (Signs compared,
+    // not multiplied: d * pl can underflow to zero.)
+    const bool away = d > 0.0f ? pl > 0.0f : pl < 0.0f;
+    if (__builtin_fabsf(d) == 0.5f && away) t += d + d;
+    return requant_band(t, zp, lo, hi);
 }
 
 }  // namespace gk

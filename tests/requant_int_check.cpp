@@ -33,16 +33,20 @@ static void check(int32_t acc, int32_t bias, float scale, int32_t zp, int32_t lo
     memcpy(&bits, &scale, 4);
     const int32_t got = gk::requant_bits(acc, bias, bits, zp, lo, hi);
     const int32_t fast = gk::requant_fast(acc, bias, scale, zp, lo, hi);
-    // the device epilogue: requant_f32 unless it flags the lane, then requant_bits
+    // the device epilogue: requant_f32, requant_f32_tie when it flags a tie,
+    // requant_bits when it flags the lane slow; a wave applies the tie tier
+    // to every lane when any lane needs it, so that tier must be exact on
+    // every lane that is not slow
     const gk::RequantF32 f = gk::requant_f32(acc, bias, scale, zp, lo, hi);
-    const int32_t dev = f.slow ? got : f.q;
+    const int32_t tq = gk::requant_f32_tie(acc, bias, scale, zp, lo, hi);
+    const int32_t dev = f.slow ? got : (f.tie ? tq : f.q);
     const int32_t want = or_requant_one(acc, bias, scale, zp, lo, hi);
     ++g_cases;
-    if (got != want || fast != want || dev != want) {
+    if (got != want || fast != want || dev != want || (!f.slow && tq != want)) {
         if (g_bad < 10)
             printf("MISMATCH acc=%d bias=%d scale=%a (0x%08x) zp=%d band=[%d,%d] bits=%d fast=%d "
-                   "dev=%d want=%d\n", acc, bias, (double)scale, bits, zp, lo, hi, got, fast, dev,
-                   want);
+                   "dev=%d tie=%d want=%d\n", acc, bias, (double)scale, bits, zp, lo, hi, got, fast,
+                   dev, tq, want);
         ++g_bad;
     }
 }
