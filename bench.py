@@ -606,6 +606,32 @@ def run_extras(args, workloads, want, timed, dev, gk, np, torch, traffic_all, or
             del bufs
         workloads["hbm_read"] = res
 
+    # the HBM write ceiling at the attention-score output size (64 x 512 x 512
+    # f32, ROTATE buffers) and over 1 GiB, nontemporal and cached stores
+    # (not in the default run)
+    if args.only == "hbm_write":
+        import ctypes
+        from gemmkit_amd import _lib
+        lib = _lib.lib()
+        res = {}
+        for label, nbytes, count in (("scores_64x512x512_f32", 64 * 512 * 512 * 4, ROTATE),
+                                     ("buf_1gib", 1 << 30, 1)):
+            bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(count)]
+            for nt in (1, 0):
+                for wgs in (1, 2, 4, 8):
+                    def call(b, wgs=wgs, nbytes=nbytes, nt=nt):
+                        rc = lib.gk_debug_write_stream(
+                            ctypes.c_void_p(b.data_ptr()), nbytes, wgs, nt,
+                            ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+                        if rc != 0:
+                            raise RuntimeError(f"gk_debug_write_stream failed: {rc}")
+                    ms = timed([lambda b=b: call(b) for b in bufs], 10 * count, warm)
+                    res[f"{label}_{'nt' if nt else 'cached'}_wg{wgs}"] = {
+                        "us": ms * 1e3, **timed.last, "GBps": nbytes / ms / 1e6,
+                        "frac_hbm": nbytes / (ms * 1e-3) / PEAK["hbm"]}
+            del bufs
+        workloads["hbm_write"] = res
+
     # a plain elementwise kernel over 1 GiB in, 1 GiB out (reads and writes
     # each byte once): the calibration workload for the HBM byte counters
     if args.only == "copy_1gib":

@@ -4,8 +4,9 @@
 // overlap.  MI355X is power-limited under such a load: the clock the chip
 // holds sets the best rate any GEMM kernel can reach, below the published
 // peak (which assumes 2.4 GHz).  Exposed as gk_debug_mfma_ceiling, beside
-// gk_debug_read_stream (a plain HBM read, the matrix-vector kernels'
-// ceiling); diagnostics with no counterpart in the reference.
+// gk_debug_read_stream and gk_debug_write_stream (plain HBM reads and
+// writes, the ceilings of the HBM-bound kernels); diagnostics with no
+// counterpart in the reference.
 #include "mma_kernel.h"
 
 #include "../../include/gemmkit_hip.h"
@@ -101,9 +102,54 @@ __global__ __launch_bounds__(256) void read_stream_kernel(const u32x4_t *__restr
     if (acc == 0x9E3779B9u) sink[blockIdx.x] = acc;
 }
 
+// A pure HBM write: the workgroups stride through `n16` 16-byte words, four
+// stores per lane per round, nontemporal (NT) or through the cache.  The
+// stored words depend on the address so nothing is constant-folded.
+template <bool NT>
+__global__ __launch_bounds__(256) void write_stream_kernel(u32x4_t *__restrict__ p, int64_t n16) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t w = (uint32_t)(i + u * stride);
+            const u32x4_t v = {w, w ^ 1u, w ^ 2u, w ^ 3u};
+            if constexpr (NT) __builtin_nontemporal_store(v, p + i + u * stride);
+            else p[i + u * stride] = v;
+        }
+    }
+    for (; i < n16; i += stride) {
+        const uint32_t w = (uint32_t)i;
+        const u32x4_t v = {w, w ^ 1u, w ^ 2u, w ^ 3u};
+        if constexpr (NT) __builtin_nontemporal_store(v, p + i);
+        else p[i] = v;
+    }
+}
+
 }  // namespace gk
 
 using namespace gk;
+
+extern "C" int gk_debug_write_stream(void *buf, int64_t bytes, int32_t wgs_per_cu,
+                                     int32_t nontemporal, void *stream) {
+    if (!buf || bytes < 16 || (bytes & 15) || wgs_per_cu < 1 || wgs_per_cu > 32 ||
+        ((uintptr_t)buf & 15))
+        return GK_ERR_ARG;
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return GK_ERR_DEVICE;
+    const int64_t n16 = bytes / 16;
+    int64_t blocks = (int64_t)(cus > 0 ? cus : 256) * wgs_per_cu;
+    if (blocks > (n16 + 255) / 256) blocks = (n16 + 255) / 256;
+    if (nontemporal)
+        hipLaunchKernelGGL(write_stream_kernel<true>, dim3((unsigned)blocks), dim3(256), 0,
+                           (hipStream_t)stream, (u32x4_t *)buf, n16);
+    else
+        hipLaunchKernelGGL(write_stream_kernel<false>, dim3((unsigned)blocks), dim3(256), 0,
+                           (hipStream_t)stream, (u32x4_t *)buf, n16);
+    return hipGetLastError() == hipSuccess ? GK_OK : GK_ERR_DEVICE;
+}
 
 extern "C" int gk_debug_read_stream(const void *buf, int64_t bytes, int32_t wgs_per_cu,
                                     void *sink, void *stream) {

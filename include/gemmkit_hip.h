@@ -78,11 +78,17 @@ int gk_debug_plan(int32_t in, int32_t kind, int64_t m, int64_t n, int64_t batch,
  * gk_debug_read_stream: enqueues, on `stream`, one pass that reads `bytes`
  * (a multiple of 16, 16-byte aligned) from `buf` and writes next to nothing
  * (`sink` holds one 32-bit word per workgroup: cus * wgs_per_cu), the HBM
- * read ceiling for a matrix-vector product of the same size. */
+ * read ceiling for a matrix-vector product of the same size.
+ *
+ * gk_debug_write_stream: enqueues, on `stream`, one pass that writes `bytes`
+ * (a multiple of 16, 16-byte aligned) of `buf`, with nontemporal stores when
+ * `nontemporal` is nonzero: the HBM write ceiling. */
 int gk_debug_mfma_ceiling(int32_t in, int64_t iters, int32_t wgs_per_cu, int32_t launches,
                           double *ops_per_s, double *clock_ghz);
 int gk_debug_read_stream(const void *buf, int64_t bytes, int32_t wgs_per_cu, void *sink,
                          void *stream);
+int gk_debug_write_stream(void *buf, int64_t bytes, int32_t wgs_per_cu, int32_t nontemporal,
+                          void *stream);
 
 /* ---------------------------------------------------------------- runtime */
 
