@@ -415,6 +415,7 @@ Tile env_tile(bool *forced) {
     if (!strcmp(s, "64x64")) return Tile::T64x64;
     if (!strcmp(s, "256x256k128")) return Tile::T256x256k128;
     if (!strcmp(s, "256x256w8k128")) return Tile::T256x256w8k128;
+    if (!strcmp(s, "128x192k128")) return Tile::T128x192k128;
     *forced = false;
     return Tile::T256x256;
 }
@@ -474,10 +475,18 @@ static const TileCand kTileCands[] = {
     {Tile::T256x256w8k128, 256, 256, 1, {0.8647, 0.8647}, 0.988872, 0.00044, 0.746808, 0.344243},
 };
 
+// The rest tile of a tail split run at a column pitch (T128x192k128): not a
+// pick_tile candidate.  Its efficiencies are set between the 128x128 tile's
+// and the 256-wide ones' (its operand reuse lies between theirs); they only
+// rank it against the two 128-wide rests, and the layer shapes it is taken
+// for were checked by measurement.
+static const TileCand kPitchedRest = {Tile::T128x192k128, 128, 192, 1, {0.78, 0.78}, 1.0, 0.0,
+                                      1.0, 0.6};
+
 // Model cost of running an M x N (x batch) product with tile c, in the units
-// of area / eff.
+// of area / eff; `pitch` > 0: the tiles advance `pitch` columns at a time.
 double tile_cost(const TileCand &c, int64_t M, int64_t N, int64_t batch, int64_t kbytes,
-                 EpiKind kind, InType in) {
+                 EpiKind kind, InType in, int64_t pitch = 0) {
     const double c_epi = kind == EpiKind::Q8 ? 0.643382
                          : kind == EpiKind::I32 ? 0.342823
                          : kind == EpiKind::F32 ? 0.301602 : 0.0;
@@ -486,7 +495,8 @@ double tile_cost(const TileCand &c, int64_t M, int64_t N, int64_t batch, int64_t
     const double kf = (double)std::max<int64_t>(kbytes, 64) / 4096.0 *
                       (in == InType::F32 ? kF32Rate : 1.0);
     const int64_t cus = g_num_cus > 0 ? g_num_cus : 256;
-    const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * batch;
+    const int64_t pn = pitch > 0 ? pitch : c.bn;
+    const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + pn - 1) / pn) * batch;
     const int64_t per_cu = (tiles + cus - 1) / cus;
     const int together = (int)std::min<int64_t>(per_cu, c.occ);
     const double area = (double)c.bm * c.bn;
@@ -499,6 +509,7 @@ double tile_cost(const TileCand &c, int64_t M, int64_t N, int64_t batch, int64_t
 const TileCand &tile_cand(Tile t) {
     for (const TileCand &c : kTileCands)
         if (c.t == t) return c;
+    if (t == kPitchedRest.t) return kPitchedRest;
     return kTileCands[0];
 }
 
@@ -520,15 +531,28 @@ Tile pick_tile(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind kind
 // Tail split.  When a product's tiles take two or more rounds of the CUs and
 // the last round is short, most CUs idle through it.  Cutting the kernel
 // frame's N so that the first part fills the full rounds exactly and running
-// the rest as a second launch with a 128-wide tile (twice the tiles, each
-// half the work) shortens that last round.  The model decides: the split is
-// taken when the two parts' modelled cost, plus one launch, beats the single
-// launch.  Only the 128-wide tiles are candidates for the rest (the model's
-// efficiencies are fitted on full rounds; among those two it ranks the
-// measured 2048 x 2816 x 4096 rests correctly).  Outputs do not change: every
-// element's K order is the same in all tiles.  GEMMKIT_HIP_TAILSPLIT=0 turns
-// it off.
-struct TailSplit { int64_t na; Tile ta, tb; };
+// the rest as a second launch with smaller tiles shortens that last round.
+// The model decides: the split is taken when the two parts' modelled cost,
+// plus one launch, beats the single launch.  Candidates for the rest: the
+// 128-wide tiles (the model's efficiencies are fitted on full rounds; among
+// those two it ranks the measured 2048 x 2816 x 4096 rests correctly), and
+// 128 x 192 tiles at a column pitch that cuts the rest into exactly one round
+// of the CUs (2048 x 2816: 16 x 16 tiles at a pitch of 176 columns).  Outputs
+// do not change: every element's K order is the same in all tiles.
+// GEMMKIT_HIP_TAILSPLIT=0 turns it off.
+struct TailSplit { int64_t na; Tile ta, tb; int32_t pn_b; };
+
+// Column pitch that runs an M x N rest as one round of T128x192k128 tiles:
+// as many tile columns as the CUs leave per tile row, the pitch a multiple of
+// 8 columns between 96 and 192; 0 when there is none.
+int32_t rest_pitch(int64_t M, int64_t N) {
+    const int64_t cus = g_num_cus > 0 ? g_num_cus : 256;
+    const int64_t tm = (M + kPitchedRest.bm - 1) / kPitchedRest.bm;
+    const int64_t tn = cus / tm;
+    if (tn < 1) return 0;
+    const int64_t p = ((N + tn - 1) / tn + 7) / 8 * 8;
+    return (p >= 96 && p <= kPitchedRest.bn) ? (int32_t)p : 0;
+}
 constexpr double kLaunchCost = 5000.0;  // one extra launch, in tile_cost units (~3 us)
 
 bool tail_split_enabled() {
@@ -549,12 +573,17 @@ bool plan_tail_split(int64_t M, int64_t N, int64_t kbytes, EpiKind kind, InType 
     const double cost_a = tile_cost(c, M, na, 1, kbytes, kind, in);
     double best_b = 1e300;
     Tile tb = Tile::T256x128;
+    int32_t pn_b = 0;
     for (Tile cand : {Tile::T256x128, Tile::T128x128}) {
         const double cb = tile_cost(tile_cand(cand), M, N - na, 1, kbytes, kind, in);
         if (cb < best_b) { best_b = cb; tb = cand; }
     }
+    if (const int32_t p = rest_pitch(M, N - na)) {
+        const double cb = tile_cost(kPitchedRest, M, N - na, 1, kbytes, kind, in, p);
+        if (cb < best_b) { best_b = cb; tb = kPitchedRest.t; pn_b = p; }
+    }
     if (cost_a + best_b + kLaunchCost >= cost_whole) return false;
-    *out = TailSplit{na, t, tb};
+    *out = TailSplit{na, t, tb, pn_b};
     return true;
 }
 
@@ -950,12 +979,14 @@ int run_fit(const Region &rg, InType in, EpiParams ep, int64_t m, int64_t k, int
     TailSplit ts;
     if (!forced && batch == 1 && tail_split_enabled() &&
         plan_tail_split(M, N, kbytes, ep.kind, in, tile, cost_whole, &ts)) {
-        // Kernel-frame columns [0, na) with the chosen tile, [na, N) with a
-        // 128-wide one: B^T rows, C columns and, for per-column channels, the
-        // scales, biases and fused biases start na further on.
+        // Kernel-frame columns [0, na) with the chosen tile, [na, N) with the
+        // rest's (at its column pitch, if any): B^T rows, C columns and, for
+        // per-column channels, the scales, biases and fused biases start na
+        // further on.
         MmaArgs a1 = args, a2 = args;
         a1.N = (int32_t)ts.na;
         a2.N = (int32_t)(N - ts.na);
+        a2.pn = ts.pn_b;
         a2.b = (const uint8_t *)Bt.p + ts.na * Bt.rs * (int64_t)esz;
         EpiParams e2 = ep;
         e2.c = (uint8_t *)ep.c + ts.na * ep.csc * osz;

@@ -65,6 +65,11 @@ struct MmaArgs {
     // element b (grid y = r, z = b) writes its partial sums to output slab
     // b*splits + r; kchunk is a multiple of 64 bytes of K.
     int32_t splits, kchunk;
+    // Column pitch of the tiles (0 = the tile's width): tile j computes
+    // columns [j*pn, j*pn + BN) and stores [j*pn, min(N, (j+1)*pn)), so a
+    // product's columns can be cut into exactly as many tiles as there are
+    // CUs for it (the overlap is computed twice and stored once).
+    int32_t pn;
 };
 
 // Tile shapes instantiated in mfma_{i8,bf16,f32}.hip.
@@ -77,6 +82,7 @@ enum class Tile : int {
     T256x128o2 = 5,  // 3-stage ring: two workgroups per CU
     T256x256k128 = 6,  // 128-byte stages, 2-stage ring
     T256x256w8k128 = 7,  // 8 waves, 128-byte stages, 2-stage ring
+    T128x192k128 = 8,  // 128-byte stages, 2-stage ring; the pitched rest of a tail split
 };
 
 hipError_t launch_mma_i8(Tile tile, const MmaArgs &args, const EpiParams &ep, hipStream_t stream);

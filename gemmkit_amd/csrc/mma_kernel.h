@@ -267,7 +267,8 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     const int wm = wave / WN, wn = wave % WN;
 
     const int tiles_m = (args.M + BM - 1) / BM;
-    const int tiles_n = (args.N + BN - 1) / BN;
+    const int PN = args.pn > 0 ? args.pn : BN;  // column pitch (<= BN)
+    const int tiles_n = (args.N + PN - 1) / PN;
     // Batch element zb, output slab z.  A batched launch remaps (tile, element)
     // pairs as one range, so the few tiles of an element share an XCD (and its
     // L2 copy of the element's operands).  SPLIT: K range blockIdx.y, and each
@@ -288,7 +289,8 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     }
     int tmi, tni;
     tile_coords(tid_logical, tiles_m, tiles_n, tmi, tni);
-    const int m0 = tmi * BM, n0 = tni * BN;
+    const int m0 = tmi * BM, n0 = tni * PN;
+    const int n_end = args.N - n0 < PN ? args.N : n0 + PN;  // columns this tile stores
     int64_t z = zb, k0 = 0, kel = args.K;
     if constexpr (SPLIT) {
         z = zb * args.splits + blockIdx.y;
@@ -624,6 +626,8 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     val_t *stg = (val_t *)smem + wave * 32 * EPI_LD;
     constexpr int CPRE = WTN / 4;          // 4-column chunks per staged row
     constexpr int RPIT = 64 / CPRE;        // rows per read iteration
+    // Lanes past RPIT*CPRE idle in the row loop (WTN = 96: 48 of 64 lanes).
+    const bool lane_on = lane < RPIT * CPRE;
     // The requantizing and the bf16 (narrowing, fused) stores are long;
     // unrolling their row loop fully would make the block loop too large to
     // unroll, and the accumulator array would then be indexed at run time
@@ -672,7 +676,7 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
         const int gcol0 = n0 + wn * WTN;
 #pragma unroll IT_UNROLL
         for (int it = 0; it < 32 / RPIT; ++it) {
-            const int row = it * RPIT + lane / CPRE;
+            const int row = it * RPIT + (lane_on ? lane / CPRE : 0);
             const int c4 = (lane % CPRE) * 4;
             v4_t v4 = *(const v4_t *)(stg + row * EPI_LD + c4);
             val_t v[4] = {v4[0], v4[1], v4[2], v4[3]};
@@ -697,8 +701,8 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
                     for (int e = 0; e < 4; ++e) f4[e] = f;
                 }
             }
-            if (grow < args.M && gcol0 + c4 < args.N)
-                store4<E, val_t, false>(ep, z, grow, gcol0 + c4, args.N, v, s4, b4, f4);
+            if (lane_on && grow < args.M && gcol0 + c4 < n_end)
+                store4<E, val_t, false>(ep, z, grow, gcol0 + c4, n_end, v, s4, b4, f4);
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_wave_barrier();
@@ -708,7 +712,9 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
 template <InType T, EpiKind E, int BM, int BN, int WM, int WN, int NS, bool SPLIT = false,
           int BK = 64>
 static hipError_t launch_one(const MmaArgs &args, const EpiParams &ep, hipStream_t stream) {
-    int tiles = ((args.M + BM - 1) / BM) * ((args.N + BN - 1) / BN);
+    const int pn = args.pn > 0 ? args.pn : BN;
+    if (pn > BN || pn % 4 != 0) return hipErrorInvalidValue;
+    int tiles = ((args.M + BM - 1) / BM) * ((args.N + pn - 1) / pn);
     dim3 grid(tiles, SPLIT ? args.splits : 1, args.batch);
     hipLaunchKernelGGL((mma_kernel<T, E, BM, BN, WM, WN, BK, NS, SPLIT>), grid,
                        dim3(WM * WN * 64), 0, stream, args, ep);
@@ -735,6 +741,7 @@ static hipError_t launch_tile(Tile tile, const MmaArgs &args, const EpiParams &e
     case Tile::T64x64: return launch_one<T, E, 64, 64, 2, 2, 4>(args, ep, stream);
     case Tile::T256x256k128: return launch_one<T, E, 256, 256, 2, 2, 2, false, 128>(args, ep, stream);
     case Tile::T256x256w8k128: return launch_one<T, E, 256, 256, 2, 4, 2, false, 128>(args, ep, stream);
+    case Tile::T128x192k128: return launch_one<T, E, 128, 192, 2, 2, 2, false, 128>(args, ep, stream);
     }
     return hipErrorInvalidValue;
 }

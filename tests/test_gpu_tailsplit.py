@@ -1,6 +1,7 @@
 """GPU parity of the tail split: products whose tiles take two rounds of the
 CUs with a short last round run as two launches (the full rounds' columns with
-the chosen tile, the rest with a 128-wide tile).  Every output element keeps
+the chosen tile, the rest with smaller tiles: 128 x 192 at a column pitch
+that makes the rest one round, on the layer shapes).  Every output element keeps
 its K order, so the results must equal the single launch
 (GEMMKIT_HIP_TAILSPLIT=0) bit for bit, for every epilogue: alpha/beta,
 requantization with per-column and per-row channels, fused bias and ReLU, and
@@ -119,3 +120,35 @@ def test_f32(dev):
         return c
     on, off = both(call)
     assert torch.equal(bits(on), bits(off))
+
+
+@pytest.mark.parametrize("kind", ["i32", "q8"])
+def test_ragged_pitched_rest(dev, kind):
+    """2000 x 11000 x 4096: the rest (2000 x 2808) runs as 16 x 16 tiles of
+    128 x 192 at a 176-column pitch, with a partial last tile row and column;
+    beta = 1 checks that the overlapping columns are stored once."""
+    m, k, n = 2000, 4096, 11000
+    plan = gk.debug_plan("i8", kind, m, n, k)
+    assert plan[1] > 0 and plan[2] == "128x192k128"
+    a, b = rand_i8(m * k, 9, dev, -127), rand_i8(n * k, 10, dev, -127)
+    if kind == "i32":
+        g = torch.Generator().manual_seed(11)
+        c0 = torch.randint(-1000, 1000, (m * n,), dtype=torch.int32, generator=g).to(dev)
+
+        def call():
+            c = c0.clone()
+            gk.gemm_i8(1, gk.MatRef.from_row_major(a, m, k), gk.MatRef(b, k, n, 1, k), 1,
+                       gk.MatMut.from_row_major(c, m, n))
+            return c
+    else:
+        g = torch.Generator().manual_seed(12)
+        scales = (1e-4 + torch.rand(n, generator=g) * (1e-2 - 1e-4)).to(dev)
+        req = gk.Requantize(gk.RequantScale.PerCol(scales), zero_point=5)
+
+        def call():
+            c = torch.zeros(m * n, dtype=torch.int8, device=dev)
+            gk.gemm_i8_requant(gk.MatRef.from_row_major(a, m, k), gk.MatRef(b, k, n, 1, k), req,
+                               gk.MatMut.from_row_major(c, m, n))
+            return c
+    on, off = both(call)
+    assert torch.equal(on, off)
