@@ -479,12 +479,18 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
 #pragma unroll
         for (int s0 = 0; s0 < NS - 1; ++s0) issue_stage(s0, s0, 0, NIW);
         wait_vmcnt<(NS - 2) * NIW>();
-    } else {
+    } else if constexpr (NS == 2) {
         // Stage 0 whole, and the first part of stage 1 (the main loop issues
         // the rest of each stage, and the first part of the one after it).
         issue_stage(0, 0, 0, NIW);
         issue_stage(1, 1, 0, P0);
         wait_vmcnt<P0>();
+    } else {
+        // Three-stage ring: stages 0 and 1 whole, the first part of stage 2.
+        issue_stage(0, 0, 0, NIW);
+        issue_stage(1, 1, 0, NIW);
+        issue_stage(2, 2, 0, P0);
+        wait_vmcnt<NIW + P0>();
     }
     if constexpr (E == EpiKind::Q8) {
 #pragma unroll
@@ -573,7 +579,51 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
         // MFMA (sched_ops).  Iterations whose loads all fall on whole stages
         // take the stage offset in the loads' scalar operand and skip the
         // per-lane tail checks.
-        static_assert(SUB == 4 && NS == 2, "four sub-steps run with a two-stage ring");
+        static_assert(SUB == 4 && (NS == 2 || NS == 3), "four sub-steps run with a 2- or 3-stage ring");
+        if constexpr (NS == 3) {
+            // Three-stage ring (the tiles small enough for three 128-byte
+            // stages in LDS): the same per-sub-step spread of the loads, but
+            // for the stage after next, into the slot of the stage before
+            // this one (free from the barrier that ended it), so every load
+            // has a whole stage more to land: iteration kt issues the rest
+            // of stage kt+2 and the first part of stage kt+3, and waits for
+            // stage kt+1 with stage kt+2's loads still in flight.
+            auto kstep3 = [&](int kt, auto whole) {
+                using L0 = std::integral_constant<int, P0>;
+                using L1 = std::integral_constant<int, P1>;
+                using L2 = std::integral_constant<int, P2>;
+                using LN = std::integral_constant<int, 0>;
+                const uint8_t *s = smem + (kt % 3) * STAGE;
+                const int lslot = (kt + 2) % 3;
+                mfmas(0);
+                ops(whole, s, 1, 1, L1{}, kt + 2, lslot, P0);
+                sched_ops<NM, NR, P1, SPAN>();
+                mfmas(1);
+                ops(whole, s, 2, 0, L2{}, kt + 2, lslot, P0 + P1);
+                sched_ops<NM, NR, P2, SPAN>();
+                mfmas(0);
+                ops(whole, s, 3, 1, LN{}, kt + 2, lslot, NIW);
+                sched_ops<NM, NR, 0, SPAN>();
+#pragma unroll
+                for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[0][i]));
+#pragma unroll
+                for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bf[0][j]));
+                wait_vmcnt<NIW>();
+                stage_barrier();
+#pragma unroll
+                for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[1][i]));
+#pragma unroll
+                for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bf[1][j]));
+                mfmas(1);
+                ops(whole, smem + ((kt + 1) % 3) * STAGE, 0, 0, L0{}, kt + 3, kt % 3, 0);
+                sched_ops<NM, NR, P0, SPAN>();
+            };
+            // Iteration kt issues stages kt+2 and kt+3.
+            const int kt_whole = soff_ok ? (ktw - 3 < KT ? (ktw - 3 > 0 ? ktw - 3 : 0) : KT) : 0;
+            int kt = 0;
+            for (; kt < kt_whole; ++kt) kstep3(kt, std::true_type{});
+            for (; kt < KT; ++kt) kstep3(kt, std::false_type{});
+        } else {
         auto kstep = [&](int kt, auto whole) {
             using L0 = std::integral_constant<int, P0>;
             using L1 = std::integral_constant<int, P1>;
@@ -609,6 +659,7 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
         int kt = 0;
         for (; kt < kt_whole; ++kt) kstep(kt, std::true_type{});
         for (; kt < KT; ++kt) kstep(kt, std::false_type{});
+        }
     }
 
     // Staged epilogue.  The MFMAs take B^T's fragment as their first operand,
@@ -741,7 +792,7 @@ static hipError_t launch_tile(Tile tile, const MmaArgs &args, const EpiParams &e
     case Tile::T64x64: return launch_one<T, E, 64, 64, 2, 2, 4>(args, ep, stream);
     case Tile::T256x256k128: return launch_one<T, E, 256, 256, 2, 2, 2, false, 128>(args, ep, stream);
     case Tile::T256x256w8k128: return launch_one<T, E, 256, 256, 2, 4, 2, false, 128>(args, ep, stream);
-    case Tile::T128x192k128: return launch_one<T, E, 128, 192, 2, 2, 2, false, 128>(args, ep, stream);
+    case Tile::T128x192k128: return launch_one<T, E, 128, 192, 2, 2, 3, false, 128>(args, ep, stream);
     }
     return hipErrorInvalidValue;
 }

@@ -52,8 +52,8 @@ def test_tail_split_of_the_layer_shapes(clean_env, shape, plan):
     # 8 x 43 tiles of 256: the first 32 tile columns fill one round of 256
     # CUs; the rest (2048 x 2816) runs as one round of 16 x 16 tiles of
     # 128 x 192 at a 176-column pitch (measured against the 128-wide rests:
-    # requantized 105.8 against 107.3 us, i32 102.0 against 103.4, bf16
-    # 163.8 against 169.8)
+    # requantized 105.5 against 108.6 us, i32 98.4 against 101.5, bf16
+    # 156.6 against 170.7)
     assert gk.debug_plan(*shape) == plan
 
 
