@@ -420,6 +420,12 @@ Tile env_tile(bool *forced) {
     return Tile::T256x256;
 }
 
+// GEMMKIT_HIP_SMALLF32=0 keeps small f32 products on split K.
+bool small_f32_enabled() {
+    const char *s = getenv("GEMMKIT_HIP_SMALLF32");
+    return !(s && !strcmp(s, "0"));
+}
+
 // GEMMKIT_HIP_KSTREAM=0 keeps short contractions on the tile kernels.
 bool kstream_enabled() {
     const char *s = getenv("GEMMKIT_HIP_KSTREAM");
@@ -858,6 +864,23 @@ int run_fit(const Region &rg, InType in, EpiParams ep, int64_t m, int64_t k, int
     if (splits > 1) {
         const int64_t kc = round_up64((k + splits - 1) / splits, 64 / (int64_t)esz);
         splits = (int)((k + kc - 1) / kc);
+    }
+    // Small f32 products that split K (too few 64 x 64 tiles for the CUs)
+    // run in one launch instead: a workgroup per 32 x 32 block with K split
+    // over its 16 waves, operands read in place (no pack, no reduction
+    // launch), when each wave's share stays short -- at most 256 k-pairs of
+    // matrix-core work per round of blocks.  By the element shape only, so a
+    // batched element takes the route of its standalone product.
+    if (in == InType::F32 && splits > 1 && small_f32_enabled()) {
+        const int64_t cus = g_num_cus > 0 ? g_num_cus : 256;
+        const int64_t blocks = ((M + 31) / 32) * ((N + 31) / 32);
+        if ((blocks + cus - 1) / cus * ((k + 31) / 32) <= 256) {
+            const SmallArgs sa{A.p, Bt.p, A.rs, A.ks, Bt.rs, Bt.ks, A.bs, Bt.bs,
+                               (int32_t)M, (int32_t)N, (int32_t)k, (int32_t)batch};
+            hipError_t e = launch_small_f32(sa, ep, tl_stream);
+            if (e != hipSuccess) return hip_fail(e, "small f32 gemm launch");
+            return finish("small f32 gemm");
+        }
     }
     const size_t a_bytes = pack_a ? pack_bytes(in, M, k, batch, A) : 0;
     const size_t b_bytes = pack_b ? pack_bytes(in, N, k, batch, Bt) : 0;

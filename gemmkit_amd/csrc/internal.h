@@ -115,6 +115,17 @@ struct GemvArgs {
     // the batch count or the grid size.
 };
 
+// Small f32 products (small.hip): one workgroup per 32 x 32 block of C, K
+// split over its sixteen waves, operands read in place.  A is M x K with element
+// (m, k) at a + m*rsa + k*ksa; B^T is N x K with element (n, k) at
+// b + n*rsb + k*ksb; batch element z at + z*bsa / z*bsb (grid y).
+struct SmallArgs {
+    const void *a, *b;
+    int64_t rsa, ksa, rsb, ksb, bsa, bsb;
+    int32_t M, N, K, batch;
+};
+hipError_t launch_small_f32(const SmallArgs &g, const EpiParams &ep, hipStream_t stream);
+
 // Batch elements one launch covers (grid z of the tiles, grid y of the
 // skinny and GEMV kernels).
 constexpr int64_t kMaxGridZ = 65535;

@@ -115,11 +115,13 @@ def test_batched_vector_route_one_launch(dev, dt, m, k, n):
         assert torch.equal(c[z * m * n:(z + 1) * m * n], one), z
 
 
-def test_batched_split_k_bounded_workspace(dev):
+def test_batched_split_k_bounded_workspace(dev, monkeypatch):
     """A batch of small, long-K f32 products keeps its per-element split (bit
     equality with the standalone call) but runs through a bounded partial-sum
     slab: 300 elements of 64x64x4096 would need 300 x 32 x 16 KiB = 150 MiB of
-    slabs at once."""
+    slabs at once.  (Split K forced: by default this shape takes the small f32
+    route, which needs no workspace.)"""
+    monkeypatch.setenv("GEMMKIT_HIP_SMALLF32", "0")
     batch, m, k, n = 300, 64, 4096, 64
     g = torch.Generator().manual_seed(5)
     a = torch.randn(batch * m * k, generator=g).to(dev)
