@@ -313,6 +313,10 @@ def main():
         "warmup": args.warmup,
         "warmup_ms_min": args.warmup_ms,
         "ms_per_step": i8_ms,
+        # spread of the per-call time over the timed replays (median above)
+        "ms_min": workloads.get("i8_gemm_4096", {}).get("ms_min"),
+        "ms_max": workloads.get("i8_gemm_4096", {}).get("ms_max"),
+        "replays": workloads.get("i8_gemm_4096", {}).get("replays"),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
