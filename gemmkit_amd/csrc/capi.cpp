@@ -20,6 +20,8 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <utility>
+#include <vector>
 
 #include <sys/syscall.h>
 #include <unistd.h>
@@ -1220,6 +1222,22 @@ int exec_requant(gk_workspace *ws, size_t m, size_t k, size_t n, const int8_t *a
                        0, 1, packed);
 }
 
+// Per-channel scale vectors this thread has checked outside graph capture
+// (the last few, by device pointer and length).
+thread_local std::vector<std::pair<const float *, size_t>> tl_checked_scales;
+
+bool scales_checked(const float *p, size_t len) {
+    for (const auto &e : tl_checked_scales)
+        if (e.first == p && e.second == len) return true;
+    return false;
+}
+
+void note_scales_checked(const float *p, size_t len) {
+    if (scales_checked(p, len)) return;
+    if (tl_checked_scales.size() >= 64) tl_checked_scales.erase(tl_checked_scales.begin());
+    tl_checked_scales.emplace_back(p, len);
+}
+
 // requant_scale / requant_bias / zero-point checks (src/adapter.rs:190-273,
 // src/api/int8.rs:291-295, :506-510).  `chan` is the channel count of the
 // chosen axis; `axis_name` is "A.rows" for the reference's per-row vectors.
@@ -1243,8 +1261,19 @@ int validate_requant(const gk_requantize *req, const gk_mat_mut *c, size_t m, si
                         req->scales_len, axis_name, chan);
         if (overlaps_bytes(c->data, c->len, 1, req->scales, req->scales_len, 4))
             return fail(GK_ERR_ALIAS, "gemmkit: requantize scales overlap C");
-        // The scale values live in device memory: copy them back to check.
-        if (chan > 0) {
+        // The scale values live in device memory: copy them back to check
+        // (the reference checks them when its RequantScale is built, and the
+        // slice stays borrowed, so they cannot change afterwards).  Under HIP
+        // graph capture nothing can be copied back: a capture accepts the
+        // scales an uncaptured call on this thread has already checked (same
+        // pointer and length), and fails with a clear error otherwise.
+        if (chan > 0 && stream_capturing()) {
+            if (!scales_checked(req->scales, chan))
+                return fail(GK_ERR_ARG,
+                            "gemmkit: requantize scales cannot be checked during HIP graph "
+                            "capture; make one uncaptured call with the same scales first, or use "
+                            "the _unchecked entry");
+        } else if (chan > 0) {
             float *h = (float *)malloc(chan * sizeof(float));
             if (!h) return fail(GK_ERR_NOMEM, "gemmkit: host allocation failed");
             hipError_t e = hipMemcpy(h, req->scales, chan * sizeof(float), hipMemcpyDeviceToHost);
@@ -1261,6 +1290,7 @@ int validate_requant(const gk_requantize *req, const gk_mat_mut *c, size_t m, si
                 }
             }
             free(h);
+            note_scales_checked(req->scales, chan);
         }
     }
     if (u8) {
