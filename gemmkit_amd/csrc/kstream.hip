@@ -11,8 +11,9 @@
 // run of 128-column tiles across it:
 //   * one producer wave loads (direct-to-LDS) the panel's A rows once and
 //     the B rows of each tile into a ring of S slots (3 for 256-byte rows, 4
-//     for shorter ones), up to S tiles ahead: a tile's loads take a memory
-//     round trip, longer than the consumers spend on a tile;
+//     for shorter ones), up to S tiles ahead (after the first tile has
+//     landed): a tile's loads take a memory round trip, longer than the
+//     consumers spend on a tile;
 //   * four consumer waves (2 x 2, 64 x 64 each) run the MFMAs of tile t from
 //     LDS, then write tile t through an LDS staging area (one 32 x 32 block at
 //     a time, as whole 128-byte row segments) while later tiles load.
@@ -109,21 +110,29 @@ __global__ __launch_bounds__(kKsThreads) void kstream_kernel(const MmaArgs args,
             load_tile(B + (int64_t)n0 * ldb_b, ldb_b, rows_b, b_lds + (t % S) * TILE);
         };
         const int rows_a = args.M - m0 < kKsTile ? args.M - m0 : kKsTile;
+        // The panel and the first tile alone at first: every workgroup of the
+        // launch needs them before any output exists, so the other tiles'
+        // loads wait until they have landed (all of Q and the first K tiles,
+        // 10 MB on the attention scores, instead of 15 MB with the ring
+        // filled at once).
         load_tile(A, lda_b, rows_a, a_lds);
-        for (int t = 0; t < S && t < ntile; ++t) load_b(t);
+        load_b(0);
         // Tile t is waited for with the loads issued after it still in flight
         // (loads complete in order; the counter holds at most 63, and waiting
         // for that many or fewer is only stronger).  Barrier t publishes it;
         // every consumer has then finished tile t-1, so its slot takes tile
-        // t-1+S.
-        int hi = (S < ntile ? S : ntile) - 1;  // last tile issued
+        // t-1+S (after barrier 0, the ring's other slots are filled).
+        int hi = 0;  // last tile issued
         for (int t = 0; t < ntile; ++t) {
             const int after = hi - t;
             if (after >= 2) wait_vmcnt<(2 * NLD < 63 ? 2 * NLD : 63)>();
             else if (after == 1) wait_vmcnt<NLD>();
             else wait_vmcnt<0>();
             stage_barrier();
-            if (t >= 1 && t - 1 + S < ntile) {
+            if (t == 0) {
+                for (int u = 1; u < S && u < ntile; ++u) load_b(u);
+                hi = (S < ntile ? S : ntile) - 1;
+            } else if (t - 1 + S < ntile) {
                 load_b(t - 1 + S);
                 hi = t - 1 + S;
             }
