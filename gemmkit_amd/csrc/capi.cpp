@@ -418,6 +418,7 @@ Tile env_tile(bool *forced) {
     if (!strcmp(s, "256x256k128")) return Tile::T256x256k128;
     if (!strcmp(s, "256x256w8k128")) return Tile::T256x256w8k128;
     if (!strcmp(s, "128x192k128")) return Tile::T128x192k128;
+    if (!strcmp(s, "128x96k128o2")) return Tile::T128x96k128o2;
     *forced = false;
     return Tile::T256x256;
 }
@@ -490,6 +491,13 @@ static const TileCand kTileCands[] = {
 // for were checked by measurement.
 static const TileCand kPitchedRest = {Tile::T128x192k128, 128, 192, 1, {0.78, 0.78}, 1.0, 0.0,
                                       1.0, 0.6};
+// The requantizing rest instead: 128 x 96 tiles, two per CU (each one's
+// requantizing epilogue runs beside the other's main loop).  Measured on the
+// 2048 x 11008 x 4096 layer: 103.2 against 106.8 us per call with the
+// 128 x 192 rest; on i32 and bf16 output it loses (103.7 against 101.1 us,
+// 161.4 against 155.2 us), so only requantized products take it.
+static const TileCand kPitchedRestQ8 = {Tile::T128x96k128o2, 128, 96, 2, {0.78, 0.78}, 1.0, 0.0,
+                                        1.0, 0.6};
 
 // Model cost of running an M x N (x batch) product with tile c, in the units
 // of area / eff; `pitch` > 0: the tiles advance `pitch` columns at a time.
@@ -518,6 +526,7 @@ const TileCand &tile_cand(Tile t) {
     for (const TileCand &c : kTileCands)
         if (c.t == t) return c;
     if (t == kPitchedRest.t) return kPitchedRest;
+    if (t == kPitchedRestQ8.t) return kPitchedRestQ8;
     return kTileCands[0];
 }
 
@@ -550,16 +559,17 @@ Tile pick_tile(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind kind
 // GEMMKIT_HIP_TAILSPLIT=0 turns it off.
 struct TailSplit { int64_t na; Tile ta, tb; int32_t pn_b; };
 
-// Column pitch that runs an M x N rest as one round of T128x192k128 tiles:
-// as many tile columns as the CUs leave per tile row, the pitch a multiple of
-// 8 columns between 96 and 192; 0 when there is none.
-int32_t rest_pitch(int64_t M, int64_t N) {
+// Column pitch that runs an M x N rest as one round of tile c (occ tiles
+// per CU): as many tile columns as the CUs leave per tile row, the pitch a
+// multiple of 8 columns between half the tile's width and its width; 0 when
+// there is none.
+int32_t rest_pitch(const TileCand &c, int64_t M, int64_t N) {
     const int64_t cus = g_num_cus > 0 ? g_num_cus : 256;
-    const int64_t tm = (M + kPitchedRest.bm - 1) / kPitchedRest.bm;
-    const int64_t tn = cus / tm;
+    const int64_t tm = (M + c.bm - 1) / c.bm;
+    const int64_t tn = cus * c.occ / tm;
     if (tn < 1) return 0;
     const int64_t p = ((N + tn - 1) / tn + 7) / 8 * 8;
-    return (p >= 96 && p <= kPitchedRest.bn) ? (int32_t)p : 0;
+    return (p >= c.bn / 2 && p <= c.bn) ? (int32_t)p : 0;
 }
 constexpr double kLaunchCost = 5000.0;  // one extra launch, in tile_cost units (~3 us)
 
@@ -586,9 +596,10 @@ bool plan_tail_split(int64_t M, int64_t N, int64_t kbytes, EpiKind kind, InType 
         const double cb = tile_cost(tile_cand(cand), M, N - na, 1, kbytes, kind, in);
         if (cb < best_b) { best_b = cb; tb = cand; }
     }
-    if (const int32_t p = rest_pitch(M, N - na)) {
-        const double cb = tile_cost(kPitchedRest, M, N - na, 1, kbytes, kind, in, p);
-        if (cb < best_b) { best_b = cb; tb = kPitchedRest.t; pn_b = p; }
+    const TileCand &pr = kind == EpiKind::Q8 ? kPitchedRestQ8 : kPitchedRest;
+    if (const int32_t p = rest_pitch(pr, M, N - na)) {
+        const double cb = tile_cost(pr, M, N - na, 1, kbytes, kind, in, p);
+        if (cb < best_b) { best_b = cb; tb = pr.t; pn_b = p; }
     }
     if (cost_a + best_b + kLaunchCost >= cost_whole) return false;
     *out = TailSplit{na, t, tb, pn_b};

@@ -82,7 +82,8 @@ enum class Tile : int {
     T256x128o2 = 5,  // 3-stage ring: two workgroups per CU
     T256x256k128 = 6,  // 128-byte stages, 2-stage ring
     T256x256w8k128 = 7,  // 8 waves, 128-byte stages, 2-stage ring
-    T128x192k128 = 8,  // 128-byte stages, 2-stage ring; the pitched rest of a tail split
+    T128x192k128 = 8,  // 128-byte stages, 3-stage ring; the pitched rest of a tail split
+    T128x96k128o2 = 9,  // 4 x 1 waves, 128-byte stages, 2-stage ring, two per CU: requantizing rests
 };
 
 hipError_t launch_mma_i8(Tile tile, const MmaArgs &args, const EpiParams &ep, hipStream_t stream);

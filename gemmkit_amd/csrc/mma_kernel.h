@@ -793,6 +793,7 @@ static hipError_t launch_tile(Tile tile, const MmaArgs &args, const EpiParams &e
     case Tile::T256x256k128: return launch_one<T, E, 256, 256, 2, 2, 2, false, 128>(args, ep, stream);
     case Tile::T256x256w8k128: return launch_one<T, E, 256, 256, 2, 4, 2, false, 128>(args, ep, stream);
     case Tile::T128x192k128: return launch_one<T, E, 128, 192, 2, 2, 3, false, 128>(args, ep, stream);
+    case Tile::T128x96k128o2: return launch_one<T, E, 128, 96, 4, 1, 2, false, 128>(args, ep, stream);
     }
     return hipErrorInvalidValue;
 }
