@@ -119,13 +119,13 @@ struct RequantF32 {
 };
 
 inline int32_t requant_band(float t, int32_t zp, int32_t lo, int32_t hi) {
-    // Anything beyond 2^24 (|zp| <= 255) lands on a band edge: clamp before
-    // converting.
-    t = __builtin_fminf(__builtin_fmaxf(t, -16777216.0f), 16777216.0f);
-    int32_t q = (int32_t)t + zp;
-    q = q < lo ? lo : q;
-    q = q > hi ? hi : q;
-    return q;
+    // Zero point and band in f32: t is an integer (or infinite), |zp| <= 255
+    // and the band lies within [-128, 255], so t + zp is exact wherever the
+    // result can land inside the band, and anything larger clamps to an edge
+    // either way.  Three instructions (add, clamp, convert).
+#pragma clang fp contract(off)
+    const float v = t + (float)zp;
+    return (int32_t)__builtin_fminf(__builtin_fmaxf(v, (float)lo), (float)hi);
 }
 
 inline RequantF32 requant_f32(int32_t acc, int32_t bias, float scale, int32_t zp, int32_t lo,
