@@ -92,19 +92,25 @@ def version() -> str:
 
 TILE_NAMES = {0: "256x256", 1: "256x128", 2: "128x128", 3: "64x64", 4: "256x256w8",
               5: "256x128o2", 6: "256x256k128", 7: "256x256w8k128", 8: "128x192k128",
-              9: "128x96k128o2"}
+              9: "128x96k128o2", 10: "256x384w8k128"}
 _IN_CODES = {"i8": 0, "bf16": 1, "f32": 2}
 _KIND_CODES = {"i32": 0, "f32": 1, "bf16": 2, "q8": 3}
 
 
-def debug_plan(in_type: str, kind: str, m: int, n: int, kbytes: int, batch: int = 1):
+def debug_plan(in_type: str, kind: str, m: int, n: int, kbytes: int, batch: int = 1,
+               pitches: bool = False):
     """Extension (no reference counterpart): the matrix-core launch plan the
     dispatcher would choose for an m x n product in the kernel frame with
     `kbytes` bytes of K per row, as (tile, na, tile_b): na > 0 means a second
-    launch covers columns [na, n) with tile_b.  Host-only."""
+    launch covers columns [na, n) with tile_b.  pitches=True: (tile, pitch,
+    na, tile_b, pitch_b), a pitch of 0 meaning the tile's width.  Host-only."""
     t, na, tb = C.c_int32(), C.c_int64(), C.c_int32()
+    pa, pb = C.c_int32(), C.c_int32()
     _check(_lib.lib().gk_debug_plan(_IN_CODES[in_type], _KIND_CODES[kind], m, n, batch, kbytes,
-                                    C.byref(t), C.byref(na), C.byref(tb)))
+                                    C.byref(t), C.byref(na), C.byref(tb), C.byref(pa),
+                                    C.byref(pb)))
+    if pitches:
+        return TILE_NAMES[t.value], pa.value, na.value, TILE_NAMES[tb.value], pb.value
     return TILE_NAMES[t.value], na.value, TILE_NAMES[tb.value]
 
 

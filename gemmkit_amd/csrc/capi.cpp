@@ -419,6 +419,7 @@ Tile env_tile(bool *forced) {
     if (!strcmp(s, "256x256w8k128")) return Tile::T256x256w8k128;
     if (!strcmp(s, "128x192k128")) return Tile::T128x192k128;
     if (!strcmp(s, "128x96k128o2")) return Tile::T128x96k128o2;
+    if (!strcmp(s, "256x384w8k128")) return Tile::T256x384w8k128;
     *forced = false;
     return Tile::T256x256;
 }
@@ -498,6 +499,17 @@ static const TileCand kPitchedRest = {Tile::T128x192k128, 128, 192, 1, {0.78, 0.
 // 161.4 against 155.2 us), so only requantized products take it.
 static const TileCand kPitchedRestQ8 = {Tile::T128x96k128o2, 128, 96, 2, {0.78, 0.78}, 1.0, 0.0,
                                         1.0, 0.6};
+// One round of 256 x 384 tiles at a column pitch (T256x384w8k128): when the
+// 256-wide tiles need more than one round of the CUs and a pitch in
+// (256, 384] covers the product in one, one launch of those tiles replaces
+// the tail split.  Measured per-CU rate (the padded columns counted) equal to
+// the 256 x 256 eight-wave tile's: 2048 x 11008 x 4096 i32 95.3 against
+// 100.3 us, requantized 104.5 against 108.2 us, bf16 159.6 against 164.5 us,
+// bf16 with f32 output 154.9 against 201.3 us, 4608 x 4608 x 4096 i32 91.8
+// against 97.8 us.  f32 inputs lose (2048 x 11008 x 4096: 1379 against
+// 1328 us) and never take it.
+static const TileCand kRoundWide = {Tile::T256x384w8k128, 256, 384, 1, {0.8647, 0.8647}, 0.988872,
+                                    0.0, 0.746808, 0.344243};
 
 // Model cost of running an M x N (x batch) product with tile c, in the units
 // of area / eff; `pitch` > 0: the tiles advance `pitch` columns at a time.
@@ -527,6 +539,7 @@ const TileCand &tile_cand(Tile t) {
         if (c.t == t) return c;
     if (t == kPitchedRest.t) return kPitchedRest;
     if (t == kPitchedRestQ8.t) return kPitchedRestQ8;
+    if (t == kRoundWide.t) return kRoundWide;
     return kTileCands[0];
 }
 
@@ -557,7 +570,7 @@ Tile pick_tile(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind kind
 // of the CUs (2048 x 2816: 16 x 16 tiles at a pitch of 176 columns).  Outputs
 // do not change: every element's K order is the same in all tiles.
 // GEMMKIT_HIP_TAILSPLIT=0 turns it off.
-struct TailSplit { int64_t na; Tile ta, tb; int32_t pn_b; };
+struct TailSplit { int64_t na; Tile ta, tb; int32_t pn_b; double cost; };
 
 // Column pitch that runs an M x N rest as one round of tile c (occ tiles
 // per CU): as many tile columns as the CUs leave per tile row, the pitch a
@@ -575,6 +588,12 @@ constexpr double kLaunchCost = 5000.0;  // one extra launch, in tile_cost units 
 
 bool tail_split_enabled() {
     const char *s = getenv("GEMMKIT_HIP_TAILSPLIT");
+    return !(s && !strcmp(s, "0"));
+}
+
+// GEMMKIT_HIP_WIDE=0 turns off the one-round 256 x 384 plan.
+bool wide_round_enabled() {
+    const char *s = getenv("GEMMKIT_HIP_WIDE");
     return !(s && !strcmp(s, "0"));
 }
 
@@ -602,8 +621,36 @@ bool plan_tail_split(int64_t M, int64_t N, int64_t kbytes, EpiKind kind, InType 
         if (cb < best_b) { best_b = cb; tb = pr.t; pn_b = p; }
     }
     if (cost_a + best_b + kLaunchCost >= cost_whole) return false;
-    *out = TailSplit{na, t, tb, pn_b};
+    *out = TailSplit{na, t, tb, pn_b, cost_a + best_b + kLaunchCost};
     return true;
+}
+
+// The launch plan of an unsplit-K product: tile `ta` over kernel-frame
+// columns [0, na) at column pitch pn_a (0: the tile's width), and, when
+// na < N, tile `tb` over [na, N) at pitch pn_b.
+struct MmaPlan { Tile ta; int32_t pn_a; int64_t na; Tile tb; int32_t pn_b; };
+
+MmaPlan plan_mma(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind kind, InType in) {
+    bool forced;
+    env_tile(&forced);
+    double cost = 0.0;
+    const Tile t = pick_tile(M, N, batch, kbytes, kind, in, &cost);
+    if (forced) {
+        const int32_t p = (t == kRoundWide.t && batch == 1) ? rest_pitch(kRoundWide, M, N) : 0;
+        return MmaPlan{t, p, N, t, 0};
+    }
+    MmaPlan plan{t, 0, N, t, 0};
+    TailSplit ts;
+    if (batch == 1 && tail_split_enabled() && plan_tail_split(M, N, kbytes, kind, in, t, cost, &ts)) {
+        plan = MmaPlan{ts.ta, 0, ts.na, ts.tb, ts.pn_b};
+        cost = ts.cost;
+    }
+    if (batch == 1 && in != InType::F32 && wide_round_enabled()) {
+        const int32_t p = rest_pitch(kRoundWide, M, N);
+        if (p > 256 && tile_cost(kRoundWide, M, N, 1, kbytes, kind, in, p) < cost)
+            plan = MmaPlan{kRoundWide.t, p, N, kRoundWide.t, 0};
+    }
+    return plan;
 }
 
 // Split K: when the 64 x 64 tiles of one product leave most CUs idle and K is
@@ -1010,30 +1057,30 @@ int run_fit(const Region &rg, InType in, EpiParams ep, int64_t m, int64_t k, int
         if (e != hipSuccess) return hip_fail(e, "kstream launch");
         return finish("mfma gemm (short K)");
     }
-    double cost_whole = 0.0;
-    const Tile tile = pick_tile(M, N, batch, kbytes, ep.kind, in, &cost_whole);
-    TailSplit ts;
-    if (!forced && batch == 1 && tail_split_enabled() &&
-        plan_tail_split(M, N, kbytes, ep.kind, in, tile, cost_whole, &ts)) {
-        // Kernel-frame columns [0, na) with the chosen tile, [na, N) with the
-        // rest's (at its column pitch, if any): B^T rows, C columns and, for
-        // per-column channels, the scales, biases and fused biases start na
-        // further on.
+    const MmaPlan plan = plan_mma(M, N, batch, kbytes, ep.kind, in);
+    if (plan.na < N) {
+        // Tail split: kernel-frame columns [0, na) with the first tile,
+        // [na, N) with the rest's (at its column pitch, if any): B^T rows, C
+        // columns and, for per-column channels, the scales, biases and fused
+        // biases start na further on.
         MmaArgs a1 = args, a2 = args;
-        a1.N = (int32_t)ts.na;
-        a2.N = (int32_t)(N - ts.na);
-        a2.pn = ts.pn_b;
-        a2.b = (const uint8_t *)Bt.p + ts.na * Bt.rs * (int64_t)esz;
+        a1.N = (int32_t)plan.na;
+        a1.pn = plan.pn_a;
+        a2.N = (int32_t)(N - plan.na);
+        a2.pn = plan.pn_b;
+        a2.b = (const uint8_t *)Bt.p + plan.na * Bt.rs * (int64_t)esz;
         EpiParams e2 = ep;
-        e2.c = (uint8_t *)ep.c + ts.na * ep.csc * osz;
-        channel_shift(e2, 1, ts.na);
-        e = launch_mma(in, ts.ta, a1, ep, tl_stream);
+        e2.c = (uint8_t *)ep.c + plan.na * ep.csc * osz;
+        channel_shift(e2, 1, plan.na);
+        e = launch_mma(in, plan.ta, a1, ep, tl_stream);
         if (e != hipSuccess) return hip_fail(e, "mfma launch");
-        e = launch_mma(in, ts.tb, a2, e2, tl_stream);
+        e = launch_mma(in, plan.tb, a2, e2, tl_stream);
         if (e != hipSuccess) return hip_fail(e, "mfma launch");
         return finish("mfma gemm (tail split)");
     }
-    e = launch_mma(in, tile, args, ep, tl_stream);
+    MmaArgs aw = args;
+    aw.pn = plan.pn_a;
+    e = launch_mma(in, plan.ta, aw, ep, tl_stream);
     if (e != hipSuccess) return hip_fail(e, "mfma launch");
     return finish("mfma gemm");
 }
@@ -1813,25 +1860,16 @@ const char *gk_last_error(void) { return tl_error.c_str(); }
 const char *gk_version(void) { return "gemmkit-hip 0.1.0 (gfx950)"; }
 
 int gk_debug_plan(int32_t in, int32_t kind, int64_t m, int64_t n, int64_t batch, int64_t kbytes,
-                  int32_t *tile, int64_t *na, int32_t *tile_b) {
+                  int32_t *tile, int64_t *na, int32_t *tile_b, int32_t *pn_a, int32_t *pn_b) {
     if (in < 0 || in > 2 || kind < 0 || kind > 3 || m <= 0 || n <= 0 || batch <= 0 ||
         kbytes < 0 || !tile || !na || !tile_b)
         return fail(GK_ERR_ARG, "gemmkit: gk_debug_plan: bad argument");
-    const InType it = (InType)in;
-    const EpiKind ek = (EpiKind)kind;
-    double cost_whole = 0.0;
-    const Tile t = pick_tile(m, n, batch, kbytes, ek, it, &cost_whole);
-    bool forced;
-    env_tile(&forced);
-    TailSplit ts;
-    *tile = (int32_t)t;
-    *na = 0;
-    *tile_b = (int32_t)t;
-    if (!forced && batch == 1 && tail_split_enabled() &&
-        plan_tail_split(m, n, kbytes, ek, it, t, cost_whole, &ts)) {
-        *na = ts.na;
-        *tile_b = (int32_t)ts.tb;
-    }
+    const MmaPlan plan = plan_mma(m, n, batch, kbytes, (EpiKind)kind, (InType)in);
+    *tile = (int32_t)plan.ta;
+    *na = plan.na < n ? plan.na : 0;
+    *tile_b = (int32_t)plan.tb;
+    if (pn_a) *pn_a = plan.pn_a;
+    if (pn_b) *pn_b = plan.pn_b;
     return ok();
 }
 

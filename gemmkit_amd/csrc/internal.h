@@ -65,10 +65,10 @@ struct MmaArgs {
     // element b (grid y = r, z = b) writes its partial sums to output slab
     // b*splits + r; kchunk is a multiple of 64 bytes of K.
     int32_t splits, kchunk;
-    // Column pitch of the tiles (0 = the tile's width): tile j computes
-    // columns [j*pn, j*pn + BN) and stores [j*pn, min(N, (j+1)*pn)), so a
-    // product's columns can be cut into exactly as many tiles as there are
-    // CUs for it (the overlap is computed twice and stored once).
+    // Column pitch of the tiles (0 = the tile's width): tile j computes and
+    // stores columns [j*pn, min(N, (j+1)*pn)), its last BN - pn B rows read
+    // as zeros, so a product's columns can be cut into exactly as many tiles
+    // as there are CUs for it.
     int32_t pn;
 };
 
@@ -84,6 +84,7 @@ enum class Tile : int {
     T256x256w8k128 = 7,  // 8 waves, 128-byte stages, 2-stage ring
     T128x192k128 = 8,  // 128-byte stages, 3-stage ring; the pitched rest of a tail split
     T128x96k128o2 = 9,  // 4 x 1 waves, 128-byte stages, 2-stage ring, two per CU: requantizing rests
+    T256x384w8k128 = 10,  // 2 x 4 waves, 128-byte stages, 2-stage ring; one round at a column pitch
 };
 
 hipError_t launch_mma_i8(Tile tile, const MmaArgs &args, const EpiParams &ep, hipStream_t stream);

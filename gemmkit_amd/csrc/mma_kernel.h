@@ -257,9 +257,15 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     // channels): with a second __shared__ array the compiler can no longer
     // tell the operand reads from the direct-to-LDS loads in flight and
     // drains every load (vmcnt(0)) before each stage's fragment reads.
+    // When the ring fills the CU's 160 KiB (256 x 384 tiles: two 80 KiB
+    // stages), the channels are staged after the main loop instead, at the
+    // ring's end, past the epilogue's staging rows (Q_LATE).
     constexpr int QCH = (E == EpiKind::Q8) ? (BM > BN ? BM : BN) : 1;
     constexpr int QBYTES = (E == EpiKind::Q8) ? QCH * 8 : 0;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM + QBYTES];
+    constexpr bool Q_LATE = SMEM + QBYTES > 160 * 1024;
+    static_assert(!Q_LATE || NWAVES * 32 * EPI_LD * 4 + QBYTES <= SMEM,
+                  "late channel staging overlaps the epilogue's rows");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[Q_LATE ? SMEM : SMEM + QBYTES];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -306,16 +312,17 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     const int KT = (int)((kbytes + BK - 1) / BK);
     const bool k_whole = (kbytes % BK) == 0;
 
-    // The tile's A rows [m0, m0+BM) and B rows [n0, n0+BN) as two buffer
+    // The tile's A rows [m0, m0+BM) and B rows [n0, n0+PN) as two buffer
     // resources spanning the valid rows' bytes (rows may overlap: a stride
-    // below the row length is a legal view).  Rows past the matrix edge start
+    // below the row length is a legal view).  Rows past the matrix edge (and
+    // B rows past the column pitch, whose outputs the next tile stores) start
     // outside them and read zeros, or, with overlapping rows, feed outputs
     // that are never stored.
     const int64_t kb16 = (kbytes + 15) / 16 * 16;
     const uint8_t *a_pan = A + (int64_t)m0 * lda_b;
     const uint8_t *b_pan = B + (int64_t)n0 * ldb_b;
     const uint32_t a_num = (uint32_t)(((args.M - m0 < BM ? args.M - m0 : BM) - 1) * lda_b + kb16);
-    const uint32_t b_num = (uint32_t)(((args.N - n0 < BN ? args.N - n0 : BN) - 1) * ldb_b + kb16);
+    const uint32_t b_num = (uint32_t)(((args.N - n0 < PN ? args.N - n0 : PN) - 1) * ldb_b + kb16);
 
     // This lane's source chunk for each of the wave's NIW load instructions:
     // instruction q fills stage bytes [q*1024, q*1024 + 1024), lane l the 16
@@ -327,15 +334,25 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     // instruction 0's and its chunk differs only through the swizzle, which
     // repeats every NPAT instructions; the offsets are then formed per load
     // from NPAT bases (fewer live registers), else kept per instruction.
+    // Otherwise, for 128-byte stages whose A rows fill whole rounds of the
+    // waves (STRIDED: the 128 x 96, 128 x 192 and 256 x 384 tiles), the
+    // wave's instruction i is instruction q = i*NWAVES + wave: instructions
+    // [0, IA) take A rows, the rest B rows, each NWAVES*RPI rows (a multiple
+    // of 32, so the same swizzle pattern) below the one before, and two base
+    // offsets serve them all.
     constexpr bool WAVE_OP = (BM % (NIW * RPI)) == 0;
+    constexpr bool STRIDED = !WAVE_OP && BK == 128 && BM % (NWAVES * RPI) == 0;
+    constexpr int IA = BM / (NWAVES * RPI);
+    static_assert(!STRIDED || (NWAVES * RPI) % 32 == 0, "strided rows must keep the swizzle");
     constexpr int NPAT = BK == 128 ? 2 : 1;
-    constexpr int NOFF = WAVE_OP ? NPAT : NIW;
+    constexpr int NOFF = WAVE_OP ? NPAT : (STRIDED ? 2 : NIW);
+    auto q_of = [&](int i) { return STRIDED ? i * NWAVES + wave : wave * NIW + i; };
     uint32_t voff[NOFF];
     int kch[NOFF];
     bool from_a[NOFF];
 #pragma unroll
     for (int i = 0; i < NOFF; ++i) {
-        const int q = wave * NIW + i;
+        const int q = q_of(STRIDED ? i * IA : i);
         const int row = q * RPI + lane / CPR;
         const int ch = (lane % CPR) ^ swz_of<BK>(row);
         kch[i] = ch * 16;
@@ -344,20 +361,27 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
                             : (uint32_t)((row - BM) * ldb_b + ch * 16);
     }
     const uint32_t rstep = (uint32_t)(RPI * (from_a[0] ? lda_b : ldb_b));
+    const uint32_t sstep_a = (uint32_t)(NWAVES * RPI * lda_b);
+    const uint32_t sstep_b = (uint32_t)(NWAVES * RPI * ldb_b);
     auto lane_off = [&](int i) -> uint32_t {
         if constexpr (WAVE_OP)
             return voff[i % NPAT] + (uint32_t)(i - i % NPAT) * rstep;
+        else if constexpr (STRIDED)
+            return i < IA ? voff[0] + (uint32_t)i * sstep_a : voff[1] + (uint32_t)(i - IA) * sstep_b;
         else
             return voff[i];
     };
-    auto lane_kch = [&](int i) { return kch[WAVE_OP ? i % NPAT : i]; };
-    auto lane_from_a = [&](int i) { return from_a[WAVE_OP ? 0 : i]; };
+    auto lane_kch = [&](int i) { return kch[WAVE_OP ? i % NPAT : (STRIDED ? (i < IA ? 0 : 1) : i)]; };
+    auto lane_from_a = [&](int i) {
+        return WAVE_OP ? from_a[0] : (STRIDED ? i < IA : from_a[i]);
+    };
+    // LDS destination of the wave's instruction i in ring slot `slot`.
+    auto dst_of = [&](int slot, int i) { return smem + slot * STAGE + q_of(i) * 1024; };
     // Loads of stage kt into ring slot `slot`.  Stages past the end of K load
     // nothing but zeros (every lane out of range), as do the chunks past K of
     // a partial last stage.
     auto issue_stage = [&](int kt, int slot, int first, int count) {
         const uint32_t kb = (uint32_t)kt * BK;
-        uint8_t *dst = smem + slot * STAGE + wave * NIW * 1024;
         const bool dead = kt >= KT;
         const bool tail = !k_whole && kt == KT - 1;
 #pragma unroll
@@ -365,7 +389,7 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
             uint32_t off = lane_off(i) + kb;
             if (dead || (tail && (int64_t)kb + lane_kch(i) >= kbytes)) off = kOutOfRange;
             dma16(lane_from_a(i) ? a_pan : b_pan, lane_from_a(i) ? a_num : b_num, off,
-                  dst + i * 1024);
+                  dst_of(slot, i));
         }
     };
     // Loads of a stage wholly inside K: the stage offset goes in the scalar
@@ -381,14 +405,13 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     const bool soff_ok = lda_b >= kb16 && ldb_b >= kb16;
     auto issue_whole = [&](int kt, int slot, int first, int count) {
         const uint32_t kb = (uint32_t)kt * BK;
-        uint8_t *dst = smem + slot * STAGE + wave * NIW * 1024;
 #pragma unroll
         for (int i = first; i < first + count; ++i) {
             if constexpr (WAVE_OP)
-                dma16s(w_pan, w_num, lane_off(i), kb, dst + i * 1024);
+                dma16s(w_pan, w_num, lane_off(i), kb, dst_of(slot, i));
             else
-                dma16s(from_a[i] ? a_pan : b_pan, from_a[i] ? a_num : b_num, voff[i], kb,
-                       dst + i * 1024);
+                dma16s(lane_from_a(i) ? a_pan : b_pan, lane_from_a(i) ? a_num : b_num,
+                       lane_off(i), kb, dst_of(slot, i));
         }
     };
 
@@ -406,6 +429,8 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     for (int j = 0; j < TN; ++j) b_row_off[j] = A_BYTES + (wn * WTN + j * 32 + lrow) * BK;
     const int swz = swz_of<BK>(lrow);  // operand block bases are multiples of 32 rows
 
+    // ASINGLE: see the 128-byte two-stage loop.
+    constexpr bool ASINGLE = BK == 128 && NS == 2 && NWAVES == 8 && TM * TN >= 12;
     v4i af[SUB][TM], bf[SUB][TN];
     auto read_frags = [&](const uint8_t *s, int ss, int set) {
         const int slot = ((2 * ss + lhalf) ^ swz) << 4;
@@ -456,8 +481,8 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     // and reach LDS after the prologue wait; the main loop's barriers publish
     // them.
     constexpr int QPT = (QCH + NWAVES * 64 - 1) / (NWAVES * 64);  // channels per thread
-    float *const q_scale = (float *)(smem + SMEM);
-    int32_t *const q_bias = (int32_t *)(smem + SMEM + QCH * 4);
+    float *const q_scale = (float *)(smem + (Q_LATE ? SMEM - QBYTES : SMEM));
+    int32_t *const q_bias = (int32_t *)(smem + (Q_LATE ? SMEM - QBYTES : SMEM) + QCH * 4);
     int q_ch0 = 0, q_n = 0;
     float q_s[QPT] = {};
     int32_t q_b[QPT] = {};
@@ -492,7 +517,7 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
         issue_stage(2, 2, 0, P0);
         wait_vmcnt<NIW + P0>();
     }
-    if constexpr (E == EpiKind::Q8) {
+    auto stage_channels = [&]() {
 #pragma unroll
         for (int u = 0; u < QPT; ++u) {
             const int c = tid + u * NWAVES * 64;
@@ -501,7 +526,8 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
                 q_bias[c] = q_b[u];
             }
         }
-    }
+    };
+    if constexpr (E == EpiKind::Q8 && !Q_LATE) stage_channels();
     stage_barrier();
     read_frags(smem, 0, 0);
 
@@ -623,6 +649,75 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
             int kt = 0;
             for (; kt < kt_whole; ++kt) kstep3(kt, std::true_type{});
             for (; kt < KT; ++kt) kstep3(kt, std::false_type{});
+        } else if constexpr (ASINGLE) {
+        // Register-tight tiles (256 x 384 on eight waves: 192 accumulator
+        // registers of the 256 a wave has at two waves per SIMD): one set of
+        // A fragments.  Each sub-step reads the next sub-step's B fragments
+        // under its first row of MFMAs and each next A fragment right after
+        // the last MFMA of its row, into the registers that row used, so only
+        // the B fragments are double-buffered.  The loads spread over the
+        // remaining MFMAs.
+        auto substep = [&](int set, auto whole, const uint8_t *src, int ss, int nset, auto nl,
+                           int st, int slot, int first) {
+            constexpr bool WHOLE = decltype(whole)::value;
+            constexpr int NL = decltype(nl)::value;
+            constexpr int NREST = NM - TN;
+            const int sl = ((2 * ss + lhalf) ^ swz) << 4;
+            int l = first;
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    acc[i][j] = M::step(bf[set][j], af[0][i], acc[i][j]);
+                    if (i == 0) bf[nset][j] = *(const v4i *)(src + b_row_off[j] + sl);
+                    const int m = i * TN + j - TN;
+                    if (m >= 0 && (m + 1) * NL / NREST != m * NL / NREST) {
+                        if constexpr (WHOLE)
+                            issue_whole(st, slot, l, 1);
+                        else
+                            issue_stage(st, slot, l, 1);
+                        ++l;
+                    }
+                }
+                af[0][i] = *(const v4i *)(src + a_row_off[i] + sl);
+            }
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+                    if (i == 0) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+                    const int m = i * TN + j - TN;
+                    if (m >= 0 && (m + 1) * NL / NREST != m * NL / NREST)
+                        __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+            }
+        };
+        auto kstep = [&](int kt, auto whole) {
+            using L0 = std::integral_constant<int, P0>;
+            using L1 = std::integral_constant<int, P1>;
+            using L2 = std::integral_constant<int, P2>;
+            using LN = std::integral_constant<int, 0>;
+            const uint8_t *s = smem + (kt & 1) * STAGE;
+            const int nslot = (kt + 1) & 1;
+            substep(0, whole, s, 1, 1, L1{}, kt + 1, nslot, P0);
+            substep(1, whole, s, 2, 0, L2{}, kt + 1, nslot, P0 + P1);
+            substep(0, whole, s, 3, 1, LN{}, kt + 1, nslot, NIW);
+#pragma unroll
+            for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bf[0][j]));
+            wait_vmcnt<0>();
+            stage_barrier();
+#pragma unroll
+            for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[0][i]));
+#pragma unroll
+            for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bf[1][j]));
+            substep(1, whole, smem + nslot * STAGE, 0, 0, L0{}, kt + 2, kt & 1, 0);
+        };
+        const int kt_whole = soff_ok ? (ktw - 2 < KT ? (ktw - 2 > 0 ? ktw - 2 : 0) : KT) : 0;
+        int kt = 0;
+        for (; kt < kt_whole; ++kt) kstep(kt, std::true_type{});
+        for (; kt < KT; ++kt) kstep(kt, std::false_type{});
         } else {
         auto kstep = [&](int kt, auto whole) {
             using L0 = std::integral_constant<int, P0>;
@@ -674,6 +769,10 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     // fraction of the rate).  The barrier also retires the zero-fill loads past
     // the end of K.
     __syncthreads();
+    if constexpr (E == EpiKind::Q8 && Q_LATE) {
+        stage_channels();
+        __syncthreads();
+    }
     val_t *stg = (val_t *)smem + wave * 32 * EPI_LD;
     constexpr int CPRE = WTN / 4;          // 4-column chunks per staged row
     constexpr int RPIT = 64 / CPRE;        // rows per read iteration
@@ -794,6 +893,7 @@ static hipError_t launch_tile(Tile tile, const MmaArgs &args, const EpiParams &e
     case Tile::T256x256w8k128: return launch_one<T, E, 256, 256, 2, 4, 2, false, 128>(args, ep, stream);
     case Tile::T128x192k128: return launch_one<T, E, 128, 192, 2, 2, 3, false, 128>(args, ep, stream);
     case Tile::T128x96k128o2: return launch_one<T, E, 128, 96, 4, 1, 2, false, 128>(args, ep, stream);
+    case Tile::T256x384w8k128: return launch_one<T, E, 256, 384, 2, 4, 2, false, 128>(args, ep, stream);
     }
     return hipErrorInvalidValue;
 }

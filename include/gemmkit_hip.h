@@ -56,11 +56,12 @@ const char *gk_version(void);
  * 1 f32, 2 bf16, 3 requantized i8/u8 output), as the dispatcher would choose
  * it with the current environment: *tile is the tile of the (first) launch,
  * *na the kernel-frame columns it covers when the product is split into two
- * launches (else 0), *tile_b the tile of the second launch.  Host-only, no
- * device needed.  No counterpart in the reference: it exposes the tile choice
- * to tests and tuning tools. */
+ * launches (else 0), *tile_b the tile of the second launch, *pn_a and *pn_b
+ * (either may be NULL) the two launches' column pitches (0: the tile's
+ * width).  Host-only, no device needed.  No counterpart in the reference: it
+ * exposes the tile choice to tests and tuning tools. */
 int gk_debug_plan(int32_t in, int32_t kind, int64_t m, int64_t n, int64_t batch, int64_t kbytes,
-                  int32_t *tile, int64_t *na, int32_t *tile_b);
+                  int32_t *tile, int64_t *na, int32_t *tile_b, int32_t *pn_a, int32_t *pn_b);
 
 /* Diagnostics with no counterpart in the reference: the ceilings the kernels
  * are measured against.

@@ -2,11 +2,13 @@
 calls, a workspace sized beforehand) and replayed several times, with eager
 work on the same buffers between the replays: each replay must reproduce the
 eager results bit for bit.  Routes: the 256 x 256 tile kernel, a packed
-operand, split K with its reduction, the tail split with its pitched rest,
-requantization, the short-contraction streaming kernel, the wavefront GEMV,
-the skinny kernel with strided activations, the small f32 kernel and a fused
-bf16 epilogue.  (No route records a memset: every scratch value is written
+operand, split K with its reduction, the one-round 256 x 384 plan and the
+tail split with its pitched rest (requantized), the short-contraction
+streaming kernel, the wavefront GEMV, the skinny kernel with strided
+activations, the small f32 kernel and a fused bf16 epilogue.  (No route records a memset: every scratch value is written
 before it is read.)"""
+import os
+
 import pytest
 import torch
 
@@ -49,16 +51,28 @@ def build_calls(dev, ws):
     calls.append(("i8 split K", c3, lambda m=m, k=k, n=n: gk.gemm_i8(
         1, gk.MatRef.from_row_major(a3, m, k), gk.MatRef(b3, k, n, 1, k), 0,
         gk.MatMut.from_row_major(c3, m, n), ws=ws)))
-    # requantized tail split with the pitched rest (2000 x 11000 x 4096)
+    # requantized 2000 x 11000 x 4096: one round of 256 x 384 tiles at a
+    # column pitch, and (GEMMKIT_HIP_WIDE=0 while the call is made) the tail
+    # split with its pitched rest
     m, k, n = 2000, 4096, 11000
     a4, b4 = _i8(m * k, 7, dev), _i8(n * k, 8, dev)
     g = torch.Generator().manual_seed(9)
     sc = (1e-4 + torch.rand(n, generator=g) * 1e-2).to(dev)
     req = gk.Requantize(gk.RequantScale.PerCol(sc), zero_point=3, relu=True)
     c4 = torch.zeros(m * n, dtype=torch.int8, device=dev)
-    calls.append(("requant tail split", c4, lambda m=m, k=k, n=n: gk.gemm_i8_requant(
+    calls.append(("requant wide round", c4, lambda m=m, k=k, n=n: gk.gemm_i8_requant(
         gk.MatRef.from_row_major(a4, m, k), gk.MatRef(b4, k, n, 1, k), req,
         gk.MatMut.from_row_major(c4, m, n), ws=ws)))
+    c4s = torch.zeros(m * n, dtype=torch.int8, device=dev)
+
+    def split_call(m=m, k=k, n=n):
+        os.environ["GEMMKIT_HIP_WIDE"] = "0"
+        try:
+            gk.gemm_i8_requant(gk.MatRef.from_row_major(a4, m, k), gk.MatRef(b4, k, n, 1, k), req,
+                               gk.MatMut.from_row_major(c4s, m, n), ws=ws)
+        finally:
+            del os.environ["GEMMKIT_HIP_WIDE"]
+    calls.append(("requant tail split", c4s, split_call))
     # batched short contraction (streaming kernel)
     bt, s, d = 8, 256, 64
     q, kk = _f(bt * s * d, 10, dev, torch.bfloat16), _f(bt * s * d, 11, dev, torch.bfloat16)
@@ -158,7 +172,7 @@ def test_every_route_replays_bit_exact(dev):
             # reset to its starting zeros) and run one route eagerly
             for _, out, _ in calls:
                 out.zero_()
-            calls[6][2]()
+            dict((nm, fn) for nm, _, fn in calls)["i8 GEMV"]()
             torch.cuda.synchronize()
             for _, out, _ in calls:
                 out.zero_()

@@ -1,9 +1,11 @@
-"""GPU parity of the tail split: products whose tiles take two rounds of the
-CUs with a short last round run as two launches (the full rounds' columns with
-the chosen tile, the rest with smaller tiles: 128 x 192 at a column pitch
-that makes the rest one round, on the layer shapes).  Every output element keeps
-its K order, so the results must equal the single launch
-(GEMMKIT_HIP_TAILSPLIT=0) bit for bit, for every epilogue: alpha/beta,
+"""GPU parity of the multi-round plans: products whose 256-wide tiles take
+two rounds of the CUs with a short last round run either as one round of
+256 x 384 tiles at a column pitch (the default where the model takes it: the
+layer shapes) or, with that plan off (GEMMKIT_HIP_WIDE=0), as a tail split
+into two launches (the full rounds' columns with the chosen tile, the rest
+with smaller tiles at a column pitch that makes the rest one round).  Every
+output element keeps its K order, so all three plans must equal the single
+launch (both off) bit for bit, for every epilogue: alpha/beta,
 requantization with per-column and per-row channels, fused bias and ReLU, and
 the orientation swap of a column-major C."""
 import os
@@ -15,25 +17,52 @@ import gemmkit_amd as gk
 
 pytestmark = pytest.mark.gpu
 
+_SWITCHES = ("GEMMKIT_HIP_WIDE", "GEMMKIT_HIP_TAILSPLIT")
 
-class split_off:
+
+class env:
+    """Sets the plan switches to `values` (others unset) for a block."""
+
+    def __init__(self, **values):
+        self.values = values
+
     def __enter__(self):
-        self.old = os.environ.get("GEMMKIT_HIP_TAILSPLIT")
-        os.environ["GEMMKIT_HIP_TAILSPLIT"] = "0"
+        self.old = {k: os.environ.get(k) for k in _SWITCHES}
+        for k in _SWITCHES:
+            os.environ.pop(k, None)
+        os.environ.update(self.values)
 
     def __exit__(self, *exc):
-        if self.old is None:
-            del os.environ["GEMMKIT_HIP_TAILSPLIT"]
-        else:
-            os.environ["GEMMKIT_HIP_TAILSPLIT"] = self.old
+        for k, v in self.old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+DEFAULT = {}
+SPLIT = {"GEMMKIT_HIP_WIDE": "0"}
+SINGLE = {"GEMMKIT_HIP_WIDE": "0", "GEMMKIT_HIP_TAILSPLIT": "0"}
+
+
+def plans(plan_args, wide=True):
+    """The plan under each setting; asserts the tail split is taken with the
+    wide plan off, and (wide=True) the wide plan by default."""
+    with env(**SPLIT):
+        assert gk.debug_plan(*plan_args)[1] > 0
+    if wide:
+        with env(**DEFAULT):
+            assert gk.debug_plan(*plan_args)[0] == "256x384w8k128"
 
 
 def both(call):
-    """Runs call() with the split on, then off; returns the two outputs."""
-    on = call()
-    with split_off():
-        off = call()
-    return on, off
+    """Runs call() under the default plan, the tail split and the single
+    launch; returns the three outputs."""
+    out = []
+    for e in (DEFAULT, SPLIT, SINGLE):
+        with env(**e):
+            out.append(call())
+    return out
 
 
 def bits(t):
@@ -51,7 +80,7 @@ def test_i8_alpha_beta(dev, c_col_major):
     m, k, n = 2048, 4096, 11008
     if c_col_major:
         m, n = n, m  # kernel frame: M = 2048, N = 11008 after the swap
-    assert gk.debug_plan("i8", "i32", 2048, 11008, k)[1] > 0
+    plans(("i8", "i32", 2048, 11008, k))
     a, b = rand_i8(m * k, 1, dev), rand_i8(k * n, 2, dev)
     g = torch.Generator().manual_seed(3)
     c0 = torch.randint(-1000, 1000, (m * n,), dtype=torch.int32, generator=g).to(dev)
@@ -62,14 +91,14 @@ def test_i8_alpha_beta(dev, c_col_major):
         c = c0.clone()
         gk.gemm_i8(3, gk.MatRef.from_row_major(a, m, k), gk.MatRef(b, k, n, 1, k), -2, C(c))
         return c
-    on, off = both(call)
-    assert torch.equal(on, off)
+    wide, split, single = both(call)
+    assert torch.equal(wide, single) and torch.equal(split, single)
 
 
 @pytest.mark.parametrize("axis,u8", [(1, False), (0, True)])
 def test_requant(dev, axis, u8):
     m, k, n = 2048, 4096, 11008
-    assert gk.debug_plan("i8", "q8", m, n, k)[1] > 0
+    plans(("i8", "q8", m, n, k))
     a, b = rand_i8(m * k, 4, dev, -127), rand_i8(n * k, 5, dev, -127)
     ch = n if axis else m
     g = torch.Generator().manual_seed(6)
@@ -85,13 +114,13 @@ def test_requant(dev, axis, u8):
         fn(gk.MatRef.from_row_major(a, m, k), gk.MatRef(b, k, n, 1, k), req,
            gk.MatMut.from_row_major(c, m, n))
         return c
-    on, off = both(call)
-    assert torch.equal(on, off)
+    wide, split, single = both(call)
+    assert torch.equal(wide, single) and torch.equal(split, single)
 
 
 def test_bf16_fused_bias_relu(dev):
     m, k, n = 2048, 4096, 11008
-    assert gk.debug_plan("bf16", "bf16", m, n, 2 * k)[1] > 0
+    plans(("bf16", "bf16", m, n, 2 * k))
     g = torch.Generator().manual_seed(7)
     a = torch.randn(m * k, generator=g).to(torch.bfloat16).to(dev)
     b = torch.randn(k * n, generator=g).to(torch.bfloat16).to(dev)
@@ -102,13 +131,13 @@ def test_bf16_fused_bias_relu(dev):
         gk.gemm_fused(1.0, gk.MatRef.from_row_major(a, m, k), gk.MatRef(b, k, n, 1, k), 0.0,
                       gk.MatMut.from_row_major(c, m, n), gk.Bias.PerCol(bias), gk.Activation.Relu)
         return c
-    on, off = both(call)
-    assert torch.equal(bits(on), bits(off))
+    wide, split, single = both(call)
+    assert torch.equal(bits(wide), bits(single)) and torch.equal(bits(split), bits(single))
 
 
 def test_f32(dev):
     m, k, n = 2048, 2048, 8448
-    assert gk.debug_plan("f32", "f32", m, n, 4 * k)[1] > 0
+    plans(("f32", "f32", m, n, 4 * k), wide=False)  # f32 inputs never take the wide plan
     g = torch.Generator().manual_seed(8)
     a = torch.rand(m * k, generator=g).to(dev) * 2 - 1
     b = torch.rand(k * n, generator=g).to(dev) * 2 - 1
@@ -118,19 +147,25 @@ def test_f32(dev):
         gk.gemm(1.0, gk.MatRef.from_row_major(a, m, k), gk.MatRef.from_row_major(b, k, n), 0.0,
                 gk.MatMut.from_row_major(c, m, n))
         return c
-    on, off = both(call)
-    assert torch.equal(bits(on), bits(off))
+    wide, split, single = both(call)
+    assert torch.equal(bits(wide), bits(single)) and torch.equal(bits(split), bits(single))
 
 
 @pytest.mark.parametrize("kind", ["i32", "q8"])
 def test_ragged_pitched_rest(dev, kind):
-    """2000 x 11000 x 4096: the rest (2000 x 2808) runs as 16 x 16 tiles of
-    128 x 192 at a 176-column pitch (i32), or 16 x 32 tiles of 128 x 96 at
-    an 88-column pitch, two per CU (requantized), with a partial last tile row
-    and column; beta = 1 checks that the overlapping columns are stored once."""
+    """2000 x 11000 x 4096: by default 8 x 32 tiles of 256 x 384 at a
+    344-column pitch; with that off, the tail split's rest (2000 x 2808) runs
+    as 16 x 16 tiles of 128 x 192 at a 176-column pitch (i32), or 16 x 32
+    tiles of 128 x 96 at an 88-column pitch, two per CU (requantized), with a
+    partial last tile row and column; beta = 1 checks that the overlapping
+    columns are stored once."""
     m, k, n = 2000, 4096, 11000
-    plan = gk.debug_plan("i8", kind, m, n, k)
-    assert plan[1] > 0 and plan[2] == ("128x96k128o2" if kind == "q8" else "128x192k128")
+    plans(("i8", kind, m, n, k))
+    with env(**SPLIT):
+        plan = gk.debug_plan("i8", kind, m, n, k)
+    assert plan[2] == ("128x96k128o2" if kind == "q8" else "128x192k128")
+    with env(**DEFAULT):
+        assert gk.debug_plan("i8", kind, m, n, k, pitches=True)[1] == 344
     a, b = rand_i8(m * k, 9, dev, -127), rand_i8(n * k, 10, dev, -127)
     if kind == "i32":
         g = torch.Generator().manual_seed(11)
@@ -151,5 +186,5 @@ def test_ragged_pitched_rest(dev, kind):
             gk.gemm_i8_requant(gk.MatRef.from_row_major(a, m, k), gk.MatRef(b, k, n, 1, k), req,
                                gk.MatMut.from_row_major(c, m, n))
             return c
-    on, off = both(call)
-    assert torch.equal(on, off)
+    wide, split, single = both(call)
+    assert torch.equal(wide, single) and torch.equal(split, single)

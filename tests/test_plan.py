@@ -1,5 +1,6 @@
 """Host-side launch plan (no device needed): the tile choice of the fitted
-cost model and the two-launch tail split, through gk_debug_plan.
+cost model, the two-launch tail split and the one-round 256 x 384 plan at a
+column pitch, through gk_debug_plan.
 
 The expected tiles are the measured best forced tiles of the 17-shape sweep the
 model was fitted to (gemmkit_amd/calibrate_tiles.py), so a refit that loses one
@@ -36,11 +37,44 @@ SWEEP = [
 def clean_env(monkeypatch):
     monkeypatch.delenv("GEMMKIT_HIP_TILE", raising=False)
     monkeypatch.delenv("GEMMKIT_HIP_TAILSPLIT", raising=False)
+    monkeypatch.delenv("GEMMKIT_HIP_WIDE", raising=False)
+
+
+@pytest.fixture
+def no_wide(clean_env, monkeypatch):
+    monkeypatch.setenv("GEMMKIT_HIP_WIDE", "0")
 
 
 @pytest.mark.parametrize("shape,best", SWEEP)
-def test_model_picks_the_measured_best_tile(clean_env, shape, best):
+def test_model_picks_the_measured_best_tile(no_wide, shape, best):
     assert gk.debug_plan(*shape)[0] == best
+
+
+@pytest.mark.parametrize("shape,pitch", [
+    (("i8", "q8", 2048, 11008, 4096), 344),
+    (("i8", "i32", 2048, 11008, 4096), 344),
+    (("bf16", "bf16", 2048, 11008, 8192), 344),
+    (("bf16", "f32", 2048, 11008, 8192), 344),
+    (("i8", "i32", 4608, 4608, 4096), 336),
+    (("i8", "q8", 2000, 11000, 4096), 344),
+])
+def test_wide_round_of_the_layer_shapes(clean_env, shape, pitch):
+    # 8 row tiles of 256 leave 32 tile columns per row for 256 CUs: 11008
+    # columns at a 344-column pitch (4608: 18 row tiles, 14 columns at 336),
+    # one launch (measured against the tail split: i32 95.3 against 100.3 us,
+    # requantized 104.5 against 108.2, bf16 159.6 against 164.5, bf16 with
+    # f32 output 154.9 against 201.3; 4608^2 91.8 against 97.8)
+    assert gk.debug_plan(*shape, pitches=True) == ("256x384w8k128", pitch, 0, "256x384w8k128", 0)
+
+
+def test_no_wide_round_when_256_wide_tiles_fit_one_round(clean_env):
+    # 4096^2: 16 x 16 tiles of 256 already make one round
+    assert gk.debug_plan("i8", "i32", 4096, 4096, 4096, pitches=True) == \
+        ("256x256k128", 0, 0, "256x256k128", 0)
+    # batched products never take it (per element shape only), nor f32
+    # inputs (2048 x 11008 x 4096: 1379 against 1328 us)
+    assert gk.debug_plan("i8", "q8", 2048, 11008, 4096, 2)[0] != "256x384w8k128"
+    assert gk.debug_plan("f32", "f32", 2048, 11008, 16384)[0] != "256x384w8k128"
 
 
 @pytest.mark.parametrize("shape,plan", [
@@ -48,7 +82,7 @@ def test_model_picks_the_measured_best_tile(clean_env, shape, best):
     (("i8", "i32", 2048, 11008, 4096), ("256x256k128", 8192, "128x192k128")),
     (("bf16", "bf16", 2048, 11008, 8192), ("256x256k128", 8192, "128x192k128")),
 ])
-def test_tail_split_of_the_layer_shapes(clean_env, shape, plan):
+def test_tail_split_of_the_layer_shapes(no_wide, shape, plan):
     # 8 x 43 tiles of 256: the first 32 tile columns fill one round of 256
     # CUs; the rest (2048 x 2816) runs as one round of 16 x 16 tiles of
     # 128 x 192 at a 176-column pitch (measured against the 128-wide rests:
@@ -63,7 +97,7 @@ def test_no_split_for_one_round(clean_env):
     assert gk.debug_plan("bf16", "f32", 4096, 4096, 8192)[1] == 0
 
 
-def test_split_switches(clean_env, monkeypatch):
+def test_split_switches(no_wide, monkeypatch):
     monkeypatch.setenv("GEMMKIT_HIP_TAILSPLIT", "0")
     assert gk.debug_plan("i8", "q8", 2048, 11008, 4096)[1] == 0
     monkeypatch.delenv("GEMMKIT_HIP_TAILSPLIT")
@@ -72,6 +106,14 @@ def test_split_switches(clean_env, monkeypatch):
     # batched products never split (the split is per element shape only)
     monkeypatch.delenv("GEMMKIT_HIP_TILE")
     assert gk.debug_plan("i8", "q8", 2048, 11008, 4096, 2)[1] == 0
+
+
+def test_forced_wide_tile_takes_the_round_pitch(clean_env, monkeypatch):
+    monkeypatch.setenv("GEMMKIT_HIP_TILE", "256x384w8k128")
+    assert gk.debug_plan("i8", "i32", 2048, 11008, 4096, pitches=True) == \
+        ("256x384w8k128", 344, 0, "256x384w8k128", 0)
+    # no pitch in [192, 384] makes one round: plain 384-wide tiles
+    assert gk.debug_plan("i8", "i32", 300, 500, 4096, pitches=True)[1] == 0
 
 
 def test_bad_arguments():
