@@ -420,6 +420,7 @@ Tile env_tile(bool *forced) {
     if (!strcmp(s, "128x192k128")) return Tile::T128x192k128;
     if (!strcmp(s, "128x96k128o2")) return Tile::T128x96k128o2;
     if (!strcmp(s, "256x384w8k128")) return Tile::T256x384w8k128;
+    if (!strcmp(s, "256x352w8k128")) return Tile::T256x352w8k128;
     *forced = false;
     return Tile::T256x256;
 }
@@ -510,6 +511,16 @@ static const TileCand kPitchedRestQ8 = {Tile::T128x96k128o2, 128, 96, 2, {0.78, 
 // 1328 us) and never take it.
 static const TileCand kRoundWide = {Tile::T256x384w8k128, 256, 384, 1, {0.8647, 0.8647}, 0.988872,
                                     0.0, 0.746808, 0.344243};
+// The same with 256 x 352 tiles (T256x352w8k128: the eight waves split the
+// first 256 columns and a 96-column strip evenly), taken first for int8
+// inputs where the pitch is at most 352: 2048 x 11008 x 4096 requantized
+// 93.3 against 100.9 us with the 384-wide tile (103.6 with the tail split),
+// i32 91.0 against 91.8 (97.0), 4608 x 4608 x 4096 86.9 against 88.6
+// (95.2).  Its main loop reads 9 fragments per 11 MFMAs against the 384-wide
+// tile's 7 per 12, and bf16 loses with it (161.6 against 155.8 us on the
+// bf16 layer), so bf16 keeps the 384-wide tile.
+static const TileCand kRoundStrip = {Tile::T256x352w8k128, 256, 352, 1, {0.8647, 0.8647},
+                                     0.988872, 0.0, 0.746808, 0.344243};
 
 // Model cost of running an M x N (x batch) product with tile c, in the units
 // of area / eff; `pitch` > 0: the tiles advance `pitch` columns at a time.
@@ -540,6 +551,7 @@ const TileCand &tile_cand(Tile t) {
     if (t == kPitchedRest.t) return kPitchedRest;
     if (t == kPitchedRestQ8.t) return kPitchedRestQ8;
     if (t == kRoundWide.t) return kRoundWide;
+    if (t == kRoundStrip.t) return kRoundStrip;
     return kTileCands[0];
 }
 
@@ -636,7 +648,8 @@ MmaPlan plan_mma(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind ki
     double cost = 0.0;
     const Tile t = pick_tile(M, N, batch, kbytes, kind, in, &cost);
     if (forced) {
-        const int32_t p = (t == kRoundWide.t && batch == 1) ? rest_pitch(kRoundWide, M, N) : 0;
+        int32_t p = 0;
+        if (batch == 1 && (t == kRoundWide.t || t == kRoundStrip.t)) p = rest_pitch(tile_cand(t), M, N);
         return MmaPlan{t, p, N, t, 0};
     }
     MmaPlan plan{t, 0, N, t, 0};
@@ -646,9 +659,16 @@ MmaPlan plan_mma(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind ki
         cost = ts.cost;
     }
     if (batch == 1 && in != InType::F32 && wide_round_enabled()) {
-        const int32_t p = rest_pitch(kRoundWide, M, N);
-        if (p > 256 && tile_cost(kRoundWide, M, N, 1, kbytes, kind, in, p) < cost)
-            plan = MmaPlan{kRoundWide.t, p, N, kRoundWide.t, 0};
+        for (const TileCand *c : {&kRoundStrip, &kRoundWide}) {
+            if (c == &kRoundStrip && in != InType::I8) continue;
+            const int32_t p = rest_pitch(*c, M, N);
+            if (p <= 256) continue;
+            const double cw = tile_cost(*c, M, N, 1, kbytes, kind, in, p);
+            if (cw < cost) {
+                plan = MmaPlan{c->t, p, N, c->t, 0};
+                cost = cw;
+            }
+        }
     }
     return plan;
 }

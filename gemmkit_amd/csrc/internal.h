@@ -85,6 +85,7 @@ enum class Tile : int {
     T128x192k128 = 8,  // 128-byte stages, 3-stage ring; the pitched rest of a tail split
     T128x96k128o2 = 9,  // 4 x 1 waves, 128-byte stages, 2-stage ring, two per CU: requantizing rests
     T256x384w8k128 = 10,  // 2 x 4 waves, 128-byte stages, 2-stage ring; one round at a column pitch
+    T256x352w8k128 = 11,  // likewise, 2 x 4 waves over 256 x 256 plus a 96-column strip
 };
 
 hipError_t launch_mma_i8(Tile tile, const MmaArgs &args, const EpiParams &ep, hipStream_t stream);

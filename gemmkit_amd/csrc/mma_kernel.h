@@ -236,18 +236,35 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<BM, BN, WM, WN, BK, NS>(),
                                    waves_per_simd<BM, BN, WM, WN, BK, NS>())))
 void mma_kernel(const MmaArgs args, const EpiParams ep) {
     constexpr int NWAVES = WM * WN;
-    constexpr int WTM = BM / WM, WTN = BN / WN;
-    constexpr int TM = WTM / 32, TN = WTN / 32;
+    // Strip tiles (STRIP: 256 x 352 on 2 x 4 waves): the wave grid covers the
+    // first BNM columns, BN/WN rounded down to whole 32-column blocks, and
+    // the SW columns past them form a strip of TS blocks per 32-row block.
+    // Wave (wm, wn) also computes the strip's row block wm*WTM + wn*32, one
+    // of its own, so every wave runs TM*TN + TS MFMAs per sub-step (11:
+    // balanced where the 11 column blocks of 352 columns cannot be split
+    // over 4 wave columns) and reads no extra A rows.
+    constexpr int SW = BN % (WN * 32);
+    constexpr bool STRIP = SW > 0;
+    constexpr int BNM = BN - SW;
+    constexpr int WTM = BM / WM, WTN = BNM / WN;
+    constexpr int TM = WTM / 32, TN = WTN / 32, TS = SW / 32;
+    static_assert(!STRIP || (SW % 32 == 0 && TM == WN && WM * WN * 32 == BM), "strip layout");
     constexpr int STAGE = (BM + BN) * BK;
     constexpr int A_BYTES = BM * BK;
     constexpr int NI = STAGE / 1024;      // direct-to-LDS instructions per stage
-    constexpr int NIW = NI / NWAVES;      // ... per wave
+    // ... per wave; when NI is not a multiple of the waves (RAGGED: the strip
+    // tile's 76), only the first NLAST waves have a real last instruction and
+    // the others issue it with every lane out of range into a spare 1 KiB.
+    constexpr int NIW = (NI + NWAVES - 1) / NWAVES;
+    constexpr int NLAST = NI - (NIW - 1) * NWAVES;
+    constexpr bool RAGGED = NLAST != NWAVES;
     constexpr int RPI = 1024 / BK;        // stage rows one instruction fills
     constexpr int CPR = BK / 16;          // 16-byte chunks per stage row
     constexpr int SUB = BK / 32;          // MFMA sub-steps per stage
-    constexpr int EPI_LD = WTN + 4;       // staged-epilogue row stride (4-byte words)
+    constexpr int EPI_W = WTN > SW ? WTN : SW;  // widest staged row (columns)
+    constexpr int EPI_LD = EPI_W + 4;     // staged-epilogue row stride (4-byte words)
     constexpr int SMEM = NS * STAGE;
-    static_assert(NI % NWAVES == 0 && TM >= 1 && TN >= 1, "tile too small");
+    static_assert((NI % NWAVES == 0 || STRIP) && TM >= 1 && TN >= 1, "tile too small");
     static_assert(NWAVES * 32 * EPI_LD * 4 <= SMEM, "epilogue staging does not fit");
     using M = Mma<T>;
     using acc_t = typename M::acc_t;
@@ -265,7 +282,8 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     constexpr bool Q_LATE = SMEM + QBYTES > 160 * 1024;
     static_assert(!Q_LATE || NWAVES * 32 * EPI_LD * 4 + QBYTES <= SMEM,
                   "late channel staging overlaps the epilogue's rows");
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[Q_LATE ? SMEM : SMEM + QBYTES];
+    constexpr int SPARE = Q_LATE ? SMEM : SMEM + QBYTES;  // RAGGED: the dummy loads' target
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[SPARE + (RAGGED ? 1024 : 0)];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -363,7 +381,13 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
     const uint32_t rstep = (uint32_t)(RPI * (from_a[0] ? lda_b : ldb_b));
     const uint32_t sstep_a = (uint32_t)(NWAVES * RPI * lda_b);
     const uint32_t sstep_b = (uint32_t)(NWAVES * RPI * ldb_b);
+    // RAGGED: this wave's last instruction is a dummy (every lane out of
+    // range, into the spare 1 KiB), so all waves issue NIW loads per stage
+    // and wait for the same counts.
+    const bool dummy_last = RAGGED && wave >= NLAST;
+    auto is_dummy = [&](int i) { return RAGGED && i == NIW - 1 && dummy_last; };
     auto lane_off = [&](int i) -> uint32_t {
+        if (is_dummy(i)) return kOutOfRange;
         if constexpr (WAVE_OP)
             return voff[i % NPAT] + (uint32_t)(i - i % NPAT) * rstep;
         else if constexpr (STRIDED)
@@ -376,7 +400,9 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
         return WAVE_OP ? from_a[0] : (STRIDED ? i < IA : from_a[i]);
     };
     // LDS destination of the wave's instruction i in ring slot `slot`.
-    auto dst_of = [&](int slot, int i) { return smem + slot * STAGE + q_of(i) * 1024; };
+    auto dst_of = [&](int slot, int i) {
+        return is_dummy(i) ? smem + SPARE : smem + slot * STAGE + q_of(i) * 1024;
+    };
     // Loads of stage kt into ring slot `slot`.  Stages past the end of K load
     // nothing but zeros (every lane out of range), as do the chunks past K of
     // a partial last stage.
@@ -387,7 +413,8 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
 #pragma unroll
         for (int i = first; i < first + count; ++i) {
             uint32_t off = lane_off(i) + kb;
-            if (dead || (tail && (int64_t)kb + lane_kch(i) >= kbytes)) off = kOutOfRange;
+            if (dead || (tail && (int64_t)kb + lane_kch(i) >= kbytes) || is_dummy(i))
+                off = kOutOfRange;
             dma16(lane_from_a(i) ? a_pan : b_pan, lane_from_a(i) ? a_num : b_num, off,
                   dst_of(slot, i));
         }
@@ -415,29 +442,43 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
         }
     };
 
-    acc_t acc[TM][TN];
+    constexpr int TSA = STRIP ? TS : 1;
+    acc_t acc[TM][TN], accs[TSA];  // accs: the strip's blocks (STRIP)
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = acc_t{};
-
-    const int lrow = lane & 31, lhalf = lane >> 5;
-    int a_row_off[TM], b_row_off[TN];
 #pragma unroll
-    for (int i = 0; i < TM; ++i) a_row_off[i] = (wm * WTM + i * 32 + lrow) * BK;
+    for (int t = 0; t < TSA; ++t) accs[t] = acc_t{};
+
+    // The wave's row block i is block rb(i) of its WTM rows: i itself, or,
+    // for strip tiles, rotated by wn, so that block 0 is the wave's strip
+    // row block.
+    auto rb = [&](int i) { return STRIP ? (i + wn) % TM : i; };
+    const int lrow = lane & 31, lhalf = lane >> 5;
+    int a_row_off[TM], b_row_off[TN], s_row_off[TSA];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) a_row_off[i] = (wm * WTM + rb(i) * 32 + lrow) * BK;
 #pragma unroll
     for (int j = 0; j < TN; ++j) b_row_off[j] = A_BYTES + (wn * WTN + j * 32 + lrow) * BK;
+#pragma unroll
+    for (int t = 0; t < TSA; ++t) s_row_off[t] = A_BYTES + (BNM + t * 32 + lrow) * BK;
     const int swz = swz_of<BK>(lrow);  // operand block bases are multiples of 32 rows
 
     // ASINGLE: see the 128-byte two-stage loop.
-    constexpr bool ASINGLE = BK == 128 && NS == 2 && NWAVES == 8 && TM * TN >= 12;
-    v4i af[SUB][TM], bf[SUB][TN];
+    constexpr bool ASINGLE = BK == 128 && NS == 2 && NWAVES == 8 && (TM * TN >= 12 || STRIP);
+    static_assert(!STRIP || ASINGLE, "strip tiles run the single-A loop");
+    v4i af[SUB][TM], bf[SUB][TN], sf[TSA];  // sf: the strip's B fragments, single set
     auto read_frags = [&](const uint8_t *s, int ss, int set) {
         const int slot = ((2 * ss + lhalf) ^ swz) << 4;
 #pragma unroll
         for (int i = 0; i < TM; ++i) af[set][i] = *(const v4i *)(s + a_row_off[i] + slot);
 #pragma unroll
         for (int j = 0; j < TN; ++j) bf[set][j] = *(const v4i *)(s + b_row_off[j] + slot);
+        if constexpr (STRIP) {
+#pragma unroll
+            for (int t = 0; t < TS; ++t) sf[t] = *(const v4i *)(s + s_row_off[t] + slot);
+        }
     };
     auto mfmas = [&](int set) {
 #pragma unroll
@@ -657,30 +698,46 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
         // the last MFMA of its row, into the registers that row used, so only
         // the B fragments are double-buffered.  The loads spread over the
         // remaining MFMAs.
+        // Strip tiles: row 0's MFMAs also run the strip's blocks (row 0 is the
+        // wave's strip row block), each strip B fragment re-read right after
+        // its MFMA (single set), all before row 0's A fragment is replaced.
         auto substep = [&](int set, auto whole, const uint8_t *src, int ss, int nset, auto nl,
                            int st, int slot, int first) {
             constexpr bool WHOLE = decltype(whole)::value;
             constexpr int NL = decltype(nl)::value;
-            constexpr int NREST = NM - TN;
+            constexpr int NFIRST = TN + (STRIP ? TS : 0);  // row 0's MFMAs
+            constexpr int NREST = NM - TN;                 // the loads spread over these
             const int sl = ((2 * ss + lhalf) ^ swz) << 4;
             int l = first;
+            auto load_after = [&](int m) {  // m: MFMA index past row 0
+                if (m >= 0 && (m + 1) * NL / NREST != m * NL / NREST) {
+                    if constexpr (WHOLE)
+                        issue_whole(st, slot, l, 1);
+                    else
+                        issue_stage(st, slot, l, 1);
+                    ++l;
+                }
+            };
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
 #pragma unroll
                 for (int j = 0; j < TN; ++j) {
                     acc[i][j] = M::step(bf[set][j], af[0][i], acc[i][j]);
                     if (i == 0) bf[nset][j] = *(const v4i *)(src + b_row_off[j] + sl);
-                    const int m = i * TN + j - TN;
-                    if (m >= 0 && (m + 1) * NL / NREST != m * NL / NREST) {
-                        if constexpr (WHOLE)
-                            issue_whole(st, slot, l, 1);
-                        else
-                            issue_stage(st, slot, l, 1);
-                        ++l;
+                    load_after(i * TN + j - TN);
+                }
+                if constexpr (STRIP) {
+                    if (i == 0) {
+#pragma unroll
+                        for (int t = 0; t < TS; ++t) {
+                            accs[t] = M::step(sf[t], af[0][0], accs[t]);
+                            sf[t] = *(const v4i *)(src + s_row_off[t] + sl);
+                        }
                     }
                 }
                 af[0][i] = *(const v4i *)(src + a_row_off[i] + sl);
             }
+            (void)NFIRST;
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -690,6 +747,13 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
                     const int m = i * TN + j - TN;
                     if (m >= 0 && (m + 1) * NL / NREST != m * NL / NREST)
                         __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
+                }
+                if (STRIP && i == 0) {
+#pragma unroll
+                    for (int t = 0; t < TS; ++t) {
+                        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+                    }
                 }
                 __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
             }
@@ -712,6 +776,10 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
             for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[0][i]));
 #pragma unroll
             for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bf[1][j]));
+            if constexpr (STRIP) {
+#pragma unroll
+                for (int t = 0; t < TS; ++t) asm volatile("" : "+v"(sf[t]));
+            }
             substep(1, whole, smem + nslot * STAGE, 0, 0, L0{}, kt + 2, kt & 1, 0);
         };
         const int kt_whole = soff_ok ? (ktw - 2 < KT ? (ktw - 2 > 0 ? ktw - 2 : 0) : KT) : 0;
@@ -774,56 +842,59 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
         __syncthreads();
     }
     val_t *stg = (val_t *)smem + wave * 32 * EPI_LD;
-    constexpr int CPRE = WTN / 4;          // 4-column chunks per staged row
-    constexpr int RPIT = 64 / CPRE;        // rows per read iteration
-    // Lanes past RPIT*CPRE idle in the row loop (WTN = 96: 48 of 64 lanes).
-    const bool lane_on = lane < RPIT * CPRE;
-    // The requantizing and the bf16 (narrowing, fused) stores are long;
-    // unrolling their row loop fully would make the block loop too large to
-    // unroll, and the accumulator array would then be indexed at run time
-    // (scratch memory).
-    constexpr int IT_UNROLL =
-        (E == EpiKind::Q8 || E == EpiKind::BF16) && 32 / RPIT > 4 ? 4 : 32 / RPIT;
-    // Requantization channels of this lane's 4 columns (fixed for the whole
-    // tile when they are columns).
-    float col_s[4] = {0, 0, 0, 0};
-    int32_t col_b[4] = {0, 0, 0, 0};
-    if constexpr (E == EpiKind::Q8) {
-        if (ep.axis) {
-            const int ci = wn * WTN + (lane % CPRE) * 4;
+    typedef val_t v4_t __attribute__((ext_vector_type(4)));
+    constexpr bool FB = E == EpiKind::F32 || E == EpiKind::BF16;
+    // Channels of this lane's 4 columns in a row of NB blocks starting at
+    // tile column lc0 (fixed for the whole row loop when they are columns):
+    // requantization scale and bias, and the fused per-column bias.
+    auto channels = [&](auto nb_c, int lc0, float (&cs)[4], int32_t (&cb)[4], float (&cf)[4]) {
+        constexpr int CPRE = decltype(nb_c)::value * 8;  // 4-column chunks per staged row
+        if constexpr (E == EpiKind::Q8) {
+            if (ep.axis) {
+                const int ci = lc0 + (lane % CPRE) * 4;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                col_s[e] = q_scale[ci + e];
-                col_b[e] = q_bias[ci + e];
+                for (int e = 0; e < 4; ++e) {
+                    cs[e] = q_scale[ci + e];
+                    cb[e] = q_bias[ci + e];
+                }
             }
         }
-    }
-    // Fused bias values of this lane's 4 columns (per-column bias), likewise.
-    constexpr bool FB = E == EpiKind::F32 || E == EpiKind::BF16;
-    float col_f[4] = {0, 0, 0, 0};
-    if constexpr (FB) {
-        if (ep.fused && ep.axis) {
-            const int cf = n0 + wn * WTN + (lane % CPRE) * 4;
+        if constexpr (FB) {
+            if (ep.fused && ep.axis) {
+                const int c = n0 + lc0 + (lane % CPRE) * 4;
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                col_f[e] = cf + e < args.N ? fused_bias<E == EpiKind::BF16>(ep, cf + e) : 0.0f;
+                for (int e = 0; e < 4; ++e)
+                    cf[e] = c + e < args.N ? fused_bias<E == EpiKind::BF16>(ep, c + e) : 0.0f;
+            }
         }
-    }
+    };
+    // One 32-row block of NB accumulator blocks (rows grow0.., tile columns
+    // lc0..): staged, then stored as rows, CPRE lanes per row.
+    auto store_rows = [&](auto nb_c, const auto &blk, int grow0, int lc0, const float (&cs)[4],
+                          const int32_t (&cb)[4], const float (&cf)[4]) {
+        constexpr int NB = decltype(nb_c)::value;
+        constexpr int CPRE = NB * 8;           // 4-column chunks per staged row
+        constexpr int RPIT = 64 / CPRE;        // rows per read iteration
+        static_assert(CPRE <= 64 && NB * 32 <= EPI_W, "staged row too wide");
+        // The requantizing and the bf16 (narrowing, fused) stores are long;
+        // unrolling their row loop fully would make the block loop too large
+        // to unroll, and the accumulator array would then be indexed at run
+        // time (scratch memory).
+        constexpr int IT_UNROLL =
+            (E == EpiKind::Q8 || E == EpiKind::BF16) && 32 / RPIT > 4 ? 4 : 32 / RPIT;
+        // Lanes past RPIT*CPRE idle in the row loop (96-column rows: 48 of 64).
+        const bool lane_on = lane < RPIT * CPRE;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-        typedef val_t v4_t __attribute__((ext_vector_type(4)));
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
+        for (int j = 0; j < NB; ++j)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const v4_t w = {(val_t)acc[i][j][4 * g], (val_t)acc[i][j][4 * g + 1],
-                                (val_t)acc[i][j][4 * g + 2], (val_t)acc[i][j][4 * g + 3]};
+                const v4_t w = {(val_t)blk[j][4 * g], (val_t)blk[j][4 * g + 1],
+                                (val_t)blk[j][4 * g + 2], (val_t)blk[j][4 * g + 3]};
                 *(v4_t *)(stg + lrow * EPI_LD + j * 32 + 8 * g + 4 * lhalf) = w;
             }
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes done
         __builtin_amdgcn_wave_barrier();
-        const int grow0 = m0 + wm * WTM + i * 32;
-        const int gcol0 = n0 + wn * WTN;
+        const int gcol0 = n0 + lc0;
 #pragma unroll IT_UNROLL
         for (int it = 0; it < 32 / RPIT; ++it) {
             const int row = it * RPIT + (lane_on ? lane / CPRE : 0);
@@ -831,8 +902,8 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
             v4_t v4 = *(const v4_t *)(stg + row * EPI_LD + c4);
             val_t v[4] = {v4[0], v4[1], v4[2], v4[3]};
             const int grow = grow0 + row;
-            float s4[4] = {col_s[0], col_s[1], col_s[2], col_s[3]};
-            int32_t b4[4] = {col_b[0], col_b[1], col_b[2], col_b[3]};
+            float s4[4] = {cs[0], cs[1], cs[2], cs[3]};
+            int32_t b4[4] = {cb[0], cb[1], cb[2], cb[3]};
             if constexpr (E == EpiKind::Q8) {
                 if (!ep.axis) {
                     const int ri = grow - q_ch0 < BM ? grow - q_ch0 : BM - 1;
@@ -843,7 +914,7 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
                     }
                 }
             }
-            float f4[4] = {col_f[0], col_f[1], col_f[2], col_f[3]};
+            float f4[4] = {cf[0], cf[1], cf[2], cf[3]};
             if constexpr (FB) {
                 if (ep.fused && !ep.axis) {
                     const float f = grow < args.M ? fused_bias<E == EpiKind::BF16>(ep, grow) : 0.0f;
@@ -856,6 +927,20 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_wave_barrier();
+    };
+    float col_s[4] = {0, 0, 0, 0}, col_f[4] = {0, 0, 0, 0};
+    int32_t col_b[4] = {0, 0, 0, 0};
+    channels(std::integral_constant<int, TN>{}, wn * WTN, col_s, col_b, col_f);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+        store_rows(std::integral_constant<int, TN>{}, acc[i], m0 + wm * WTM + rb(i) * 32, wn * WTN,
+                   col_s, col_b, col_f);
+    if constexpr (STRIP) {
+        float st_s[4] = {0, 0, 0, 0}, st_f[4] = {0, 0, 0, 0};
+        int32_t st_b[4] = {0, 0, 0, 0};
+        channels(std::integral_constant<int, TS>{}, BNM, st_s, st_b, st_f);
+        store_rows(std::integral_constant<int, TS>{}, accs, m0 + wm * WTM + wn * 32, BNM, st_s,
+                   st_b, st_f);
     }
 }
 
@@ -894,6 +979,7 @@ static hipError_t launch_tile(Tile tile, const MmaArgs &args, const EpiParams &e
     case Tile::T128x192k128: return launch_one<T, E, 128, 192, 2, 2, 3, false, 128>(args, ep, stream);
     case Tile::T128x96k128o2: return launch_one<T, E, 128, 96, 4, 1, 2, false, 128>(args, ep, stream);
     case Tile::T256x384w8k128: return launch_one<T, E, 256, 384, 2, 4, 2, false, 128>(args, ep, stream);
+    case Tile::T256x352w8k128: return launch_one<T, E, 256, 352, 2, 4, 2, false, 128>(args, ep, stream);
     }
     return hipErrorInvalidValue;
 }

@@ -2,7 +2,7 @@
 calls, a workspace sized beforehand) and replayed several times, with eager
 work on the same buffers between the replays: each replay must reproduce the
 eager results bit for bit.  Routes: the 256 x 256 tile kernel, a packed
-operand, split K with its reduction, the one-round 256 x 384 plan and the
+operand, split K with its reduction, the one-round 256 x 352 plan and the
 tail split with its pitched rest (requantized), the short-contraction
 streaming kernel, the wavefront GEMV, the skinny kernel with strided
 activations, the small f32 kernel and a fused bf16 epilogue.  (No route records a memset: every scratch value is written
@@ -51,7 +51,7 @@ def build_calls(dev, ws):
     calls.append(("i8 split K", c3, lambda m=m, k=k, n=n: gk.gemm_i8(
         1, gk.MatRef.from_row_major(a3, m, k), gk.MatRef(b3, k, n, 1, k), 0,
         gk.MatMut.from_row_major(c3, m, n), ws=ws)))
-    # requantized 2000 x 11000 x 4096: one round of 256 x 384 tiles at a
+    # requantized 2000 x 11000 x 4096: one round of 256 x 352 tiles at a
     # column pitch, and (GEMMKIT_HIP_WIDE=0 while the call is made) the tail
     # split with its pitched rest
     m, k, n = 2000, 4096, 11000

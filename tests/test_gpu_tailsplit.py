@@ -1,11 +1,12 @@
 """GPU parity of the multi-round plans: products whose 256-wide tiles take
 two rounds of the CUs with a short last round run either as one round of
-256 x 384 tiles at a column pitch (the default where the model takes it: the
-layer shapes) or, with that plan off (GEMMKIT_HIP_WIDE=0), as a tail split
-into two launches (the full rounds' columns with the chosen tile, the rest
-with smaller tiles at a column pitch that makes the rest one round).  Every
-output element keeps its K order, so all three plans must equal the single
-launch (both off) bit for bit, for every epilogue: alpha/beta,
+256 x 352 strip tiles (int8) or 256 x 384 tiles (bf16, or a pitch past 352)
+at a column pitch (the default where the model takes it: the layer shapes;
+both tiles are also forced here with GEMMKIT_HIP_TILE) or, with that plan off (GEMMKIT_HIP_WIDE=0), as a tail
+split into two launches (the full rounds' columns with the chosen tile, the
+rest with smaller tiles at a column pitch that makes the rest one round).
+Every output element keeps its K order, so all five plans must equal the
+single launch (both off) bit for bit, for every epilogue: alpha/beta,
 requantization with per-column and per-row channels, fused bias and ReLU, and
 the orientation swap of a column-major C."""
 import os
@@ -17,7 +18,7 @@ import gemmkit_amd as gk
 
 pytestmark = pytest.mark.gpu
 
-_SWITCHES = ("GEMMKIT_HIP_WIDE", "GEMMKIT_HIP_TAILSPLIT")
+_SWITCHES = ("GEMMKIT_HIP_WIDE", "GEMMKIT_HIP_TAILSPLIT", "GEMMKIT_HIP_TILE")
 
 
 class env:
@@ -41,25 +42,30 @@ class env:
 
 
 DEFAULT = {}
+WIDE384 = {"GEMMKIT_HIP_TILE": "256x384w8k128"}
+STRIP352 = {"GEMMKIT_HIP_TILE": "256x352w8k128"}
 SPLIT = {"GEMMKIT_HIP_WIDE": "0"}
 SINGLE = {"GEMMKIT_HIP_WIDE": "0", "GEMMKIT_HIP_TAILSPLIT": "0"}
 
 
 def plans(plan_args, wide=True):
     """The plan under each setting; asserts the tail split is taken with the
-    wide plan off, and (wide=True) the wide plan by default."""
+    wide plan off, and (wide=True) the one-round plan by default: 256 x 352
+    strip tiles for int8, 256 x 384 tiles for bf16."""
     with env(**SPLIT):
         assert gk.debug_plan(*plan_args)[1] > 0
     if wide:
         with env(**DEFAULT):
-            assert gk.debug_plan(*plan_args)[0] == "256x384w8k128"
+            want = "256x352w8k128" if plan_args[0] == "i8" else "256x384w8k128"
+            assert gk.debug_plan(*plan_args)[0] == want
 
 
 def both(call):
-    """Runs call() under the default plan, the tail split and the single
-    launch; returns the three outputs."""
+    """Runs call() under the default plan, the forced 256 x 384 and 256 x 352
+    tiles, the tail split and the single launch; returns (default, 384, 352,
+    split, single)."""
     out = []
-    for e in (DEFAULT, SPLIT, SINGLE):
+    for e in (DEFAULT, WIDE384, STRIP352, SPLIT, SINGLE):
         with env(**e):
             out.append(call())
     return out
@@ -91,8 +97,9 @@ def test_i8_alpha_beta(dev, c_col_major):
         c = c0.clone()
         gk.gemm_i8(3, gk.MatRef.from_row_major(a, m, k), gk.MatRef(b, k, n, 1, k), -2, C(c))
         return c
-    wide, split, single = both(call)
-    assert torch.equal(wide, single) and torch.equal(split, single)
+    *plans_out, single = both(call)
+    for o in plans_out:
+        assert torch.equal(o, single)
 
 
 @pytest.mark.parametrize("axis,u8", [(1, False), (0, True)])
@@ -114,8 +121,9 @@ def test_requant(dev, axis, u8):
         fn(gk.MatRef.from_row_major(a, m, k), gk.MatRef(b, k, n, 1, k), req,
            gk.MatMut.from_row_major(c, m, n))
         return c
-    wide, split, single = both(call)
-    assert torch.equal(wide, single) and torch.equal(split, single)
+    *plans_out, single = both(call)
+    for o in plans_out:
+        assert torch.equal(o, single)
 
 
 def test_bf16_fused_bias_relu(dev):
@@ -131,8 +139,9 @@ def test_bf16_fused_bias_relu(dev):
         gk.gemm_fused(1.0, gk.MatRef.from_row_major(a, m, k), gk.MatRef(b, k, n, 1, k), 0.0,
                       gk.MatMut.from_row_major(c, m, n), gk.Bias.PerCol(bias), gk.Activation.Relu)
         return c
-    wide, split, single = both(call)
-    assert torch.equal(bits(wide), bits(single)) and torch.equal(bits(split), bits(single))
+    *plans_out, single = both(call)
+    for o in plans_out:
+        assert torch.equal(bits(o), bits(single))
 
 
 def test_f32(dev):
@@ -147,14 +156,15 @@ def test_f32(dev):
         gk.gemm(1.0, gk.MatRef.from_row_major(a, m, k), gk.MatRef.from_row_major(b, k, n), 0.0,
                 gk.MatMut.from_row_major(c, m, n))
         return c
-    wide, split, single = both(call)
-    assert torch.equal(bits(wide), bits(single)) and torch.equal(bits(split), bits(single))
+    *plans_out, single = both(call)
+    for o in plans_out:
+        assert torch.equal(bits(o), bits(single))
 
 
 @pytest.mark.parametrize("kind", ["i32", "q8"])
 def test_ragged_pitched_rest(dev, kind):
-    """2000 x 11000 x 4096: by default 8 x 32 tiles of 256 x 384 at a
-    344-column pitch; with that off, the tail split's rest (2000 x 2808) runs
+    """2000 x 11000 x 4096: by default 8 x 32 tiles of 256 x 352 at a
+    344-column pitch (partial last tile row); with that off, the tail split's rest (2000 x 2808) runs
     as 16 x 16 tiles of 128 x 192 at a 176-column pitch (i32), or 16 x 32
     tiles of 128 x 96 at an 88-column pitch, two per CU (requantized), with a
     partial last tile row and column; beta = 1 checks that the overlapping
@@ -186,5 +196,6 @@ def test_ragged_pitched_rest(dev, kind):
             gk.gemm_i8_requant(gk.MatRef.from_row_major(a, m, k), gk.MatRef(b, k, n, 1, k), req,
                                gk.MatMut.from_row_major(c, m, n))
             return c
-    wide, split, single = both(call)
-    assert torch.equal(wide, single) and torch.equal(split, single)
+    *plans_out, single = both(call)
+    for o in plans_out:
+        assert torch.equal(o, single)

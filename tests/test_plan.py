@@ -50,21 +50,26 @@ def test_model_picks_the_measured_best_tile(no_wide, shape, best):
     assert gk.debug_plan(*shape)[0] == best
 
 
-@pytest.mark.parametrize("shape,pitch", [
-    (("i8", "q8", 2048, 11008, 4096), 344),
-    (("i8", "i32", 2048, 11008, 4096), 344),
-    (("bf16", "bf16", 2048, 11008, 8192), 344),
-    (("bf16", "f32", 2048, 11008, 8192), 344),
-    (("i8", "i32", 4608, 4608, 4096), 336),
-    (("i8", "q8", 2000, 11000, 4096), 344),
+@pytest.mark.parametrize("shape,pitch,tile", [
+    (("i8", "q8", 2048, 11008, 4096), 344, "256x352w8k128"),
+    (("i8", "i32", 2048, 11008, 4096), 344, "256x352w8k128"),
+    (("bf16", "bf16", 2048, 11008, 8192), 344, "256x384w8k128"),
+    (("bf16", "f32", 2048, 11008, 8192), 344, "256x384w8k128"),
+    (("i8", "i32", 4608, 4608, 4096), 336, "256x352w8k128"),
+    (("i8", "q8", 2000, 11000, 4096), 344, "256x352w8k128"),
 ])
-def test_wide_round_of_the_layer_shapes(clean_env, shape, pitch):
+def test_wide_round_of_the_layer_shapes(clean_env, shape, pitch, tile):
     # 8 row tiles of 256 leave 32 tile columns per row for 256 CUs: 11008
     # columns at a 344-column pitch (4608: 18 row tiles, 14 columns at 336),
-    # one launch (measured against the tail split: i32 95.3 against 100.3 us,
-    # requantized 104.5 against 108.2, bf16 159.6 against 164.5, bf16 with
-    # f32 output 154.9 against 201.3; 4608^2 91.8 against 97.8)
-    assert gk.debug_plan(*shape, pitches=True) == ("256x384w8k128", pitch, 0, "256x384w8k128", 0)
+    # one launch of 256 x 352 strip tiles (int8) or 256 x 384 tiles (bf16:
+    # the strip tile's main loop loses there)
+    assert gk.debug_plan(*shape, pitches=True) == (tile, pitch, 0, tile, 0)
+
+
+def test_wide_round_past_352_takes_the_384_tile(clean_env):
+    # 2048 x 12000: 32 tile columns at a 376-column pitch
+    assert gk.debug_plan("i8", "i32", 2048, 12000, 4096, pitches=True) == \
+        ("256x384w8k128", 376, 0, "256x384w8k128", 0)
 
 
 def test_no_wide_round_when_256_wide_tiles_fit_one_round(clean_env):
@@ -112,6 +117,9 @@ def test_forced_wide_tile_takes_the_round_pitch(clean_env, monkeypatch):
     monkeypatch.setenv("GEMMKIT_HIP_TILE", "256x384w8k128")
     assert gk.debug_plan("i8", "i32", 2048, 11008, 4096, pitches=True) == \
         ("256x384w8k128", 344, 0, "256x384w8k128", 0)
+    monkeypatch.setenv("GEMMKIT_HIP_TILE", "256x352w8k128")
+    assert gk.debug_plan("i8", "i32", 2048, 11008, 4096, pitches=True) == \
+        ("256x352w8k128", 344, 0, "256x352w8k128", 0)
     # no pitch in [192, 384] makes one round: plain 384-wide tiles
     assert gk.debug_plan("i8", "i32", 300, 500, 4096, pitches=True)[1] == 0
 
