@@ -421,6 +421,7 @@ Tile env_tile(bool *forced) {
     if (!strcmp(s, "128x96k128o2")) return Tile::T128x96k128o2;
     if (!strcmp(s, "256x384w8k128")) return Tile::T256x384w8k128;
     if (!strcmp(s, "256x352w8k128")) return Tile::T256x352w8k128;
+    if (!strcmp(s, "256x256w8m16")) return Tile::T256x256w8m16;
     *forced = false;
     return Tile::T256x256;
 }
@@ -476,14 +477,16 @@ static bool gemv_beats_skinny(InType in, int64_t short_side, int64_t kbytes) {
 // tile is the best measured one on each shape.
 struct TileCand { Tile t; int bm, bn, occ; double eff[2], eff_i8, hide, epi, epi_q8; };
 static const TileCand kTileCands[] = {
-    {Tile::T256x256, 256, 256, 1, {0.85303, 0.85303}, 1.0, 0.088032, 1.0, 1.0},
-    {Tile::T256x256w8, 256, 256, 1, {0.858816, 0.858816}, 1.121781, 5.3e-05, 0.94197, 0.728267},
-    {Tile::T256x128o2, 256, 128, 2, {0.666828, 0.618457}, 1.011653, 0.324247, 0.602712, 0.847837},
-    {Tile::T256x128, 256, 128, 1, {0.67676, 0.67676}, 1.026106, 0.0, 0.49797, 1.00419},
-    {Tile::T128x128, 128, 128, 2, {0.714723, 0.570162}, 0.974166, 0.826374, 1.166487, 0.4006},
-    {Tile::T64x64, 64, 64, 2, {0.493576, 0.455552}, 0.738895, 0.831829, 0.2, 0.2},
-    {Tile::T256x256k128, 256, 256, 1, {0.863509, 0.863509}, 1.3, 0.01624, 1.105762, 1.290751},
-    {Tile::T256x256w8k128, 256, 256, 1, {0.8647, 0.8647}, 0.988872, 0.00044, 0.746808, 0.344243},
+    {Tile::T256x256, 256, 256, 1, {0.817513, 0.817513}, 1.0, 0.307445, 1.0, 1.0},
+    {Tile::T256x256w8, 256, 256, 1, {0.798817, 0.798817}, 1.3, 0.1715, 1.144686, 0.968081},
+    {Tile::T256x128o2, 256, 128, 2, {0.609198, 0.580406}, 0.950117, 0.464277, 0.66113, 0.740229},
+    {Tile::T256x128, 256, 128, 1, {0.616949, 0.616949}, 1.026287, 0.0, 0.665666, 1.02864},
+    {Tile::T128x128, 128, 128, 2, {0.616337, 0.540289}, 0.95272, 0.598733, 0.429867, 0.2},
+    {Tile::T64x64, 64, 64, 2, {0.409374, 0.411763}, 0.709875, 0.812048, 0.2, 0.2},
+    {Tile::T256x256k128, 256, 256, 1, {0.805722, 0.805722}, 1.3, 0.322672, 1.286801, 1.334919},
+    {Tile::T256x256w8k128, 256, 256, 1, {0.821426, 0.821426}, 1.278928, 0.196392, 0.992329,
+     0.969417},
+    {Tile::T256x256w8m16, 256, 256, 1, {0.882658, 0.882658}, 1.3, 0.290227, 1.068566, 0.956933},
 };
 
 // The rest tile of a tail split run at a column pitch (T128x192k128): not a
@@ -509,8 +512,8 @@ static const TileCand kPitchedRestQ8 = {Tile::T128x96k128o2, 128, 96, 2, {0.78, 
 // bf16 with f32 output 154.9 against 201.3 us, 4608 x 4608 x 4096 i32 91.8
 // against 97.8 us.  f32 inputs lose (2048 x 11008 x 4096: 1379 against
 // 1328 us) and never take it.
-static const TileCand kRoundWide = {Tile::T256x384w8k128, 256, 384, 1, {0.8647, 0.8647}, 0.988872,
-                                    0.0, 0.746808, 0.344243};
+static const TileCand kRoundWide = {Tile::T256x384w8k128, 256, 384, 1, {0.821426, 0.821426},
+                                    1.278928, 0.0, 0.992329, 0.969417};
 // The same with 256 x 352 tiles (T256x352w8k128: the eight waves split the
 // first 256 columns and a 96-column strip evenly), taken first for int8
 // inputs where the pitch is at most 352: 2048 x 11008 x 4096 requantized
@@ -519,18 +522,18 @@ static const TileCand kRoundWide = {Tile::T256x384w8k128, 256, 384, 1, {0.8647, 
 // (95.2).  Its main loop reads 9 fragments per 11 MFMAs against the 384-wide
 // tile's 7 per 12, and bf16 loses with it (161.6 against 155.8 us on the
 // bf16 layer), so bf16 keeps the 384-wide tile.
-static const TileCand kRoundStrip = {Tile::T256x352w8k128, 256, 352, 1, {0.8647, 0.8647},
-                                     0.988872, 0.0, 0.746808, 0.344243};
+static const TileCand kRoundStrip = {Tile::T256x352w8k128, 256, 352, 1, {0.821426, 0.821426},
+                                     1.278928, 0.0, 0.992329, 0.969417};
 
 // Model cost of running an M x N (x batch) product with tile c, in the units
 // of area / eff; `pitch` > 0: the tiles advance `pitch` columns at a time.
 double tile_cost(const TileCand &c, int64_t M, int64_t N, int64_t batch, int64_t kbytes,
                  EpiKind kind, InType in, int64_t pitch = 0) {
-    const double c_epi = kind == EpiKind::Q8 ? 0.643382
-                         : kind == EpiKind::I32 ? 0.342823
-                         : kind == EpiKind::F32 ? 0.301602 : 0.0;
-    constexpr double kTileLatency = 13829.251;  // in the units of area / eff
-    constexpr double kF32Rate = 4.562511;    // f32 main-loop cost per K byte vs i8/bf16
+    const double c_epi = kind == EpiKind::Q8 ? 0.602342
+                         : kind == EpiKind::I32 ? 0.40104
+                         : kind == EpiKind::F32 ? 0.251808 : 0.0;
+    constexpr double kTileLatency = 11604.671;  // in the units of area / eff
+    constexpr double kF32Rate = 4.530131;       // f32 main-loop cost per K byte vs i8/bf16
     const double kf = (double)std::max<int64_t>(kbytes, 64) / 4096.0 *
                       (in == InType::F32 ? kF32Rate : 1.0);
     const int64_t cus = g_num_cus > 0 ? g_num_cus : 256;
@@ -555,6 +558,18 @@ const TileCand &tile_cand(Tile t) {
     return kTileCands[0];
 }
 
+// The 16x16-MFMA tile (T256x256w8m16): int8 and bf16 inputs only (no f32
+// variant).  Its bf16 sums take 32 k per instruction, the other tiles' 16,
+// so bf16 results differ between it and them in the last bits: short bf16
+// contractions stay on the 32x32 tiles, bit-identical to the streaming
+// kernel that serves them.  GEMMKIT_HIP_M16=0 turns it off.
+bool m16_allowed(InType in, int64_t kbytes) {
+    const char *s = getenv("GEMMKIT_HIP_M16");
+    if (s && !strcmp(s, "0")) return false;
+    if (in == InType::F32) return false;
+    return in == InType::I8 || kbytes > kstream_max_kbytes();
+}
+
 Tile pick_tile(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind kind, InType in,
                double *cost_out = nullptr) {
     bool forced;
@@ -563,6 +578,7 @@ Tile pick_tile(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind kind
     double best = 1e300;
     Tile bt = Tile::T64x64;
     for (const TileCand &c : kTileCands) {
+        if (c.t == Tile::T256x256w8m16 && !m16_allowed(in, kbytes)) continue;
         const double cost = tile_cost(c, M, N, batch, kbytes, kind, in);
         if (cost < best * 0.999) { best = cost; bt = c.t; }
     }
@@ -611,6 +627,9 @@ bool wide_round_enabled() {
 
 bool plan_tail_split(int64_t M, int64_t N, int64_t kbytes, EpiKind kind, InType in, Tile t,
                      double cost_whole, TailSplit *out) {
+    // bf16: the split's launches all sum in the 32x32 tiles' order, so the
+    // split equals the one-round wide plan bit for bit.
+    if (in == InType::BF16 && t == Tile::T256x256w8m16) t = Tile::T256x256w8k128;
     const TileCand &c = tile_cand(t);
     const int64_t cus = g_num_cus > 0 ? g_num_cus : 256;
     const int64_t tiles_m = (M + c.bm - 1) / c.bm, tiles_n = (N + c.bn - 1) / c.bn;
@@ -658,15 +677,18 @@ MmaPlan plan_mma(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind ki
         plan = MmaPlan{ts.ta, 0, ts.na, ts.tb, ts.pn_b};
         cost = ts.cost;
     }
+    // One round of wide tiles: taken whenever it exists with at most 15% of
+    // its columns padding (every such shape measured beat the tail split and
+    // the single launch: the layers by 5-25%; the model, whose wide-tile
+    // constants are the 256 x 256 eight-wave tile's, cannot rank them).
     if (batch == 1 && in != InType::F32 && wide_round_enabled()) {
         for (const TileCand *c : {&kRoundStrip, &kRoundWide}) {
             if (c == &kRoundStrip && in != InType::I8) continue;
             const int32_t p = rest_pitch(*c, M, N);
             if (p <= 256) continue;
-            const double cw = tile_cost(*c, M, N, 1, kbytes, kind, in, p);
-            if (cw < cost) {
+            if (p * 100 >= c->bn * 85) {
                 plan = MmaPlan{c->t, p, N, c->t, 0};
-                cost = cw;
+                break;
             }
         }
     }

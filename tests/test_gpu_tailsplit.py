@@ -127,6 +127,9 @@ def test_requant(dev, axis, u8):
 
 
 def test_bf16_fused_bias_relu(dev):
+    """bf16: the one-round plans and the tail split sum in the 32x32 tiles'
+    order (bit-identical); the single launch takes the 16x16-MFMA tile,
+    which sums 32 k per instruction, so it agrees within the bf16 bars."""
     m, k, n = 2048, 4096, 11008
     plans(("bf16", "bf16", m, n, 2 * k))
     g = torch.Generator().manual_seed(7)
@@ -140,8 +143,13 @@ def test_bf16_fused_bias_relu(dev):
                       gk.MatMut.from_row_major(c, m, n), gk.Bias.PerCol(bias), gk.Activation.Relu)
         return c
     *plans_out, single = both(call)
-    for o in plans_out:
-        assert torch.equal(bits(o), bits(single))
+    for o in plans_out[1:]:
+        assert torch.equal(bits(o), bits(plans_out[0]))
+    with env(**SINGLE):
+        assert gk.debug_plan("bf16", "bf16", m, n, 2 * k)[0] == "256x256w8m16"
+    ref, got = plans_out[0].float(), single.float()
+    floor = 1e-3 * ref.abs().max()
+    assert ((got - ref).abs() <= 1e-2 * torch.maximum(ref.abs(), floor)).all()
 
 
 def test_f32(dev):

@@ -1,9 +1,10 @@
 """GPU parity of every matrix-core tile, each forced with GEMMKIT_HIP_TILE
 (which also turns off split K, the tail split and the streaming kernel), on
 ragged shapes: i8 with alpha/beta and requantized outputs bit-exact against
-the oracle; bf16 and f32 outputs identical across all tiles (every tile feeds
-each output's K chunks to the matrix cores in the same order) and within the
-float bars against the f64 product."""
+the oracle; bf16 and f32 outputs identical across all 32x32-MFMA tiles (every
+one feeds each output's K chunks to the matrix cores in the same order) and
+within the float bars against the f64 product; the 16x16-MFMA tile (bf16
+only: it sums 32 k per instruction) within the same bars."""
 import os
 
 import numpy as np
@@ -17,6 +18,7 @@ from helpers import to_dev
 pytestmark = pytest.mark.gpu
 
 TILES = sorted(gk.TILE_NAMES.values())
+M16 = "256x256w8m16"  # 16x16 MFMAs: int8 and bf16 inputs only
 
 
 class tile:
@@ -83,6 +85,8 @@ def test_float_tiles_identical(dev, dt):
     c0 = torch.randn(m * n, generator=g).to(dev)
     outs = {}
     for name in TILES:
+        if name == M16 and dt == torch.float32:
+            continue
         c = c0.clone()
         with tile(name):
             if dt == torch.bfloat16:
@@ -92,10 +96,12 @@ def test_float_tiles_identical(dev, dt):
                 gk.gemm(0.5, gk.MatRef.from_row_major(a, m, k), gk.MatRef(b, k, n, 1, k), 1.0,
                         gk.MatMut.from_row_major(c, m, n))
         outs[name] = c
-    first = outs[TILES[0]]
-    for name in TILES[1:]:
+    same = [t for t in TILES if t != M16]
+    first = outs[same[0]]
+    for name in same[1:]:
         assert torch.equal(outs[name], first), name
     ref = 0.5 * (a.double().cpu().reshape(m, k) @ b.double().cpu().reshape(n, k).T) + \
         c0.double().cpu().reshape(m, n)
-    err = (first.double().cpu().reshape(m, n) - ref).norm() / ref.norm()
-    assert err <= (1e-5 if dt == torch.float32 else 1e-2)
+    for name in [same[0]] + ([M16] if M16 in outs else []):
+        err = (outs[name].double().cpu().reshape(m, n) - ref).norm() / ref.norm()
+        assert err <= (1e-5 if dt == torch.float32 else 1e-2), name

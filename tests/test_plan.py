@@ -13,16 +13,16 @@ import gemmkit_amd as gk
 
 # (in, output kind, M, N, K bytes, batch) -> measured best tile
 SWEEP = [
-    (("i8", "i32", 4096, 4096, 4096, 1), "256x256k128"),
-    (("i8", "q8", 2048, 11008, 4096, 1), "256x256w8k128"),
-    (("i8", "i32", 2048, 11008, 4096, 1), "256x256k128"),
-    (("i8", "i32", 8192, 8192, 1024, 1), "128x128"),
+    (("i8", "i32", 4096, 4096, 4096, 1), "256x256w8m16"),
+    (("i8", "q8", 2048, 11008, 4096, 1), "256x256w8m16"),
+    (("i8", "i32", 2048, 11008, 4096, 1), "256x256w8m16"),
+    (("i8", "i32", 8192, 8192, 1024, 1), "256x256w8m16"),
     (("i8", "i32", 1024, 1024, 8192, 1), "64x64"),
-    (("i8", "i32", 3000, 5000, 2000, 1), "256x256k128"),
-    (("i8", "q8", 4096, 4096, 4096, 1), "256x256w8k128"),
-    (("bf16", "f32", 4096, 4096, 8192, 1), "256x256w8k128"),
+    (("i8", "i32", 3000, 5000, 2000, 1), "256x256w8m16"),
+    (("i8", "q8", 4096, 4096, 4096, 1), "256x256w8m16"),
+    (("bf16", "f32", 4096, 4096, 8192, 1), "256x256w8m16"),
     (("bf16", "f32", 512, 512, 256, 64), "256x256w8k128"),
-    (("bf16", "bf16", 2048, 11008, 8192, 1), "256x256k128"),
+    (("bf16", "bf16", 2048, 11008, 8192, 1), "256x256w8m16"),
     (("bf16", "bf16", 2048, 2048, 4096, 1), "128x128"),
     (("f32", "f32", 2048, 2048, 8192, 1), "128x128"),
     (("f32", "f32", 1024, 1024, 4096, 1), "64x64"),
@@ -38,6 +38,7 @@ def clean_env(monkeypatch):
     monkeypatch.delenv("GEMMKIT_HIP_TILE", raising=False)
     monkeypatch.delenv("GEMMKIT_HIP_TAILSPLIT", raising=False)
     monkeypatch.delenv("GEMMKIT_HIP_WIDE", raising=False)
+    monkeypatch.delenv("GEMMKIT_HIP_M16", raising=False)
 
 
 @pytest.fixture
@@ -45,9 +46,25 @@ def no_wide(clean_env, monkeypatch):
     monkeypatch.setenv("GEMMKIT_HIP_WIDE", "0")
 
 
+@pytest.fixture
+def pick_only(no_wide, monkeypatch):
+    monkeypatch.setenv("GEMMKIT_HIP_TAILSPLIT", "0")
+
+
 @pytest.mark.parametrize("shape,best", SWEEP)
-def test_model_picks_the_measured_best_tile(no_wide, shape, best):
+def test_model_picks_the_measured_best_tile(pick_only, shape, best):
     assert gk.debug_plan(*shape)[0] == best
+
+
+def test_m16_tile_exclusions(pick_only, monkeypatch):
+    # no f32 variant of the 16x16-MFMA tile
+    assert gk.debug_plan("f32", "f32", 4096, 4096, 16384)[0] != "256x256w8m16"
+    # bf16 contractions of at most 256 bytes stay on the 32x32 tiles (the
+    # streaming kernel's summation order); int8 sums are exact either way
+    assert gk.debug_plan("bf16", "f32", 4096, 4096, 256)[0] != "256x256w8m16"
+    assert gk.debug_plan("bf16", "f32", 4096, 4096, 1024)[0] == "256x256w8m16"
+    monkeypatch.setenv("GEMMKIT_HIP_M16", "0")
+    assert gk.debug_plan("i8", "i32", 4096, 4096, 4096)[0] != "256x256w8m16"
 
 
 @pytest.mark.parametrize("shape,pitch,tile", [
@@ -75,7 +92,7 @@ def test_wide_round_past_352_takes_the_384_tile(clean_env):
 def test_no_wide_round_when_256_wide_tiles_fit_one_round(clean_env):
     # 4096^2: 16 x 16 tiles of 256 already make one round
     assert gk.debug_plan("i8", "i32", 4096, 4096, 4096, pitches=True) == \
-        ("256x256k128", 0, 0, "256x256k128", 0)
+        ("256x256w8m16", 0, 0, "256x256w8m16", 0)
     # batched products never take it (per element shape only), nor f32
     # inputs (2048 x 11008 x 4096: 1379 against 1328 us)
     assert gk.debug_plan("i8", "q8", 2048, 11008, 4096, 2)[0] != "256x384w8k128"
@@ -83,9 +100,10 @@ def test_no_wide_round_when_256_wide_tiles_fit_one_round(clean_env):
 
 
 @pytest.mark.parametrize("shape,plan", [
-    (("i8", "q8", 2048, 11008, 4096), ("256x256w8k128", 8192, "128x96k128o2")),
-    (("i8", "i32", 2048, 11008, 4096), ("256x256k128", 8192, "128x192k128")),
-    (("bf16", "bf16", 2048, 11008, 8192), ("256x256k128", 8192, "128x192k128")),
+    (("i8", "q8", 2048, 11008, 4096), ("256x256w8m16", 8192, "128x96k128o2")),
+    (("i8", "i32", 2048, 11008, 4096), ("256x256w8m16", 8192, "128x192k128")),
+    # bf16 splits keep the 32x32 tiles' summation order throughout
+    (("bf16", "bf16", 2048, 11008, 8192), ("256x256w8k128", 8192, "128x192k128")),
 ])
 def test_tail_split_of_the_layer_shapes(no_wide, shape, plan):
     # 8 x 43 tiles of 256: the first 32 tile columns fill one round of 256
