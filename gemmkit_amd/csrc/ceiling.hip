@@ -171,7 +171,7 @@ extern "C" int gk_debug_read_stream(const void *buf, int64_t bytes, int32_t wgs_
 extern "C" int gk_debug_mfma_ceiling(int32_t in_type, int64_t iters, int32_t wgs_per_cu,
                                      int32_t launches, double *ops_per_s, double *clock_ghz) {
     if (!ops_per_s || !clock_ghz || iters < 1 || wgs_per_cu != 1 ||
-        launches < 1 || (in_type != 0 && in_type != 1))
+        launches < 1 || in_type < 0 || in_type > 3)
         return GK_ERR_ARG;
     int dev = 0;
     hipDeviceProp_t prop;
@@ -198,9 +198,12 @@ extern "C" int gk_debug_mfma_ceiling(int32_t in_type, int64_t iters, int32_t wgs
         if (in_type == 0)
             hipLaunchKernelGGL(mfma_ceiling_kernel<InType::I8>, dim3(blocks), dim3(256), 0,
                                nullptr, iters, sink, clocks);
-        else
+        else if (in_type == 1)
             hipLaunchKernelGGL(mfma_ceiling_kernel<InType::BF16>, dim3(blocks), dim3(256), 0,
                                nullptr, iters, sink, clocks);
+        else
+            (void)launch_mfma16_ceiling(in_type == 2 ? InType::I8 : InType::BF16, blocks, iters,
+                                        sink, clocks);
         (void)hipEventRecord(e1, nullptr);
         if (hipGetLastError() != hipSuccess || hipEventSynchronize(e1) != hipSuccess)
             rc = GK_ERR_DEVICE;
@@ -214,9 +217,11 @@ extern "C" int gk_debug_mfma_ceiling(int32_t in_type, int64_t iters, int32_t wgs
     (void)hipFree(sink);
     (void)hipFree(clocks);
     if (rc != GK_OK) return rc;
-    // 16 MFMAs of 2*32*32*32 (i8) or 2*32*32*16 (bf16) operations per round
-    const double per_mfma = in_type == 0 ? 65536.0 : 32768.0;
-    const double ops = (double)blocks * 4 * 16 * per_mfma * (double)iters;
+    // per round: 16 MFMAs of 2*32*32*32 (i8) or 2*32*32*16 (bf16) operations,
+    // or 32 of 2*16*16*64 (i8) or 2*16*16*32 (bf16)
+    const double per_round = in_type == 0 ? 16 * 65536.0 : in_type == 1 ? 16 * 32768.0
+                           : in_type == 2 ? 32 * 32768.0 : 32 * 16384.0;
+    const double ops = (double)blocks * 4 * per_round * (double)iters;
     *ops_per_s = ops / (ms * 1e-3);
     *clock_ghz = c[1] ? (double)c[0] / (double)c[1] * 0.1 : 0.0;
     return GK_OK;

@@ -68,13 +68,14 @@ int gk_debug_plan(int32_t in, int32_t kind, int64_t m, int64_t n, int64_t batch,
  *
  * gk_debug_mfma_ceiling: every CU issues back-to-back MFMAs on random
  * register operands (in: 0 int8 v_mfma_i32_32x32x32_i8, 1 bf16
- * v_mfma_f32_32x32x16_bf16), `iters` rounds of 16 per wave, one 4-wave
- * workgroup per CU (wgs_per_cu must be 1: its 256 accumulator registers per
- * lane leave room for one wave per SIMD), `launches` launches of which the last
- * is timed (the ones before bring the clocks to their loaded state).  Returns
- * the achieved rate (ops/s) and the shader clock the chip held (from the
- * shader and real-time counters): how far below the published peak the power
- * limit puts any GEMM kernel.
+ * v_mfma_f32_32x32x16_bf16, 16 per round into 16 32x32 blocks; 2 int8
+ * v_mfma_i32_16x16x64_i8, 3 bf16 v_mfma_f32_16x16x32_bf16, 32 per round into
+ * 32 16x16 blocks), `iters` rounds per wave, one 4-wave workgroup per CU
+ * (wgs_per_cu must be 1: one wave per SIMD), `launches` launches of which the
+ * last is timed (the ones before bring the clocks to their loaded state).
+ * Returns the achieved rate (ops/s) and the shader clock the chip held (from
+ * the shader and real-time counters): how far below the published peak the
+ * power limit puts a GEMM kernel built on that instruction.
  *
  * gk_debug_read_stream: enqueues, on `stream`, one pass that reads `bytes`
  * (a multiple of 16, 16-byte aligned) from `buf` and writes next to nothing
