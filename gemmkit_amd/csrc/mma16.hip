@@ -168,7 +168,7 @@ void mma16_kernel(const MmaArgs args, const EpiParams ep) {
             for (int j = 0; j < TN; ++j) acc[i][j] = M::step(bf[set][j], af[set][i], acc[i][j]);
     };
     // Program-order memory operations of a phase: A reads of blocks
-    // [alo, alo+NA), then (WB) the B reads, with NL loads of stage st into
+    // [alo, alo+NA) and (WB) the B reads, with NL loads of stage st into
     // `slot` spread among them (op_is_load); whole stages take scalar-offset
     // loads.
     auto ops = [&](auto whole, const uint8_t *src, int ss, int set, int alo, auto na, auto wb,
@@ -182,10 +182,16 @@ void mma16_kernel(const MmaArgs args, const EpiParams ep) {
         int l = first;
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
-            if (r < NA)
-                af[set][alo + r] = *(const v4i *)(src + a_off0 + (alo + r) * 16 * BK + sl);
+            // Order: A[alo], the B fragments, then A[alo+1 ..]: the next
+            // phase's first MFMAs pair A[alo] with every B fragment (measured
+            // on int8 4096^3: 58.4-58.9 against 58.6-60.7 us with the A
+            // fragments first).
+            const int ra = r == 0 ? 0 : (r <= NB ? -1 : r - NB);
+            const int rbi = r - (NA > 0 ? 1 : 0);
+            if (NA > 0 && ra >= 0)
+                af[set][alo + ra] = *(const v4i *)(src + a_off0 + (alo + ra) * 16 * BK + sl);
             else
-                bf[set][r - NA] = *(const v4i *)(src + b_off0 + (r - NA) * 16 * BK + sl);
+                bf[set][rbi] = *(const v4i *)(src + b_off0 + rbi * 16 * BK + sl);
             if ((r + 1) * NL / NR != r * NL / NR) {
                 if constexpr (WHOLE)
                     issue_whole(st, slot, l, 1);
