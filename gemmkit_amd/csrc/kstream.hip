@@ -49,7 +49,7 @@ __device__ __forceinline__ int ks_slot(int r, int c) {
 // that the plain kernel loads nothing in the consumers: a bias load would
 // make the compiler wait for the wave's outstanding stores (loads and stores
 // share one counter) at every block, even where the call has no bias
-// (attention scores 16.5 against 13 us).
+// (attention scores 16.95-17.5 against 17.5-17.95 us on one box).
 template <InType T, EpiKind E, int KB, bool FUSED>
 __global__ __launch_bounds__(kKsThreads) void kstream_kernel(const MmaArgs args, const EpiParams ep,
                                                              int tiles_m, int tiles_n, int chunk,
