@@ -105,3 +105,40 @@ def test_float_tiles_identical(dev, dt):
     for name in [same[0]] + ([M16] if M16 in outs else []):
         err = (outs[name].double().cpu().reshape(m, n) - ref).norm() / ref.norm()
         assert err <= (1e-5 if dt == torch.float32 else 1e-2), name
+
+
+@pytest.mark.parametrize("name", TILES)
+def test_batched_bf16_every_tile(dev, name):
+    """Each element of a batched bf16 product (grid z, B shared through a zero
+    batch stride, C element stride past its extent) equals its standalone
+    call on the same forced tile, bit for bit, with f32 and bf16 output."""
+    batch, m, k, n = 3, 270, 320, 300
+    g = torch.Generator().manual_seed(0x7B1)
+    a = torch.randn(batch * m * k, generator=g).to(torch.bfloat16).to(dev)
+    b = torch.randn(k * n, generator=g).to(torch.bfloat16).to(dev)
+    cbs = m * n + 64
+    for out in (torch.float32, torch.bfloat16):
+        c = torch.zeros(batch * cbs, dtype=out, device=dev)
+        with tile(name):
+            if out == torch.float32:
+                gk.gemm_batched_bf16_f32out(batch, 0.75, gk.MatRef.from_row_major(a, m, k), m * k,
+                                            gk.MatRef(b, k, n, 1, k), 0, 0.0,
+                                            gk.MatMut.from_row_major(c, m, n), cbs)
+            else:
+                gk.gemm_batched(batch, 0.75, gk.MatRef.from_row_major(a, m, k), m * k,
+                                gk.MatRef(b, k, n, 1, k), 0, 0.0,
+                                gk.MatMut.from_row_major(c, m, n), cbs)
+            for z in range(batch):
+                s = torch.zeros(m * n, dtype=out, device=dev)
+                az = a[z * m * k:(z + 1) * m * k]
+                if out == torch.float32:
+                    gk.gemm_bf16_f32out(0.75, gk.MatRef.from_row_major(az, m, k),
+                                        gk.MatRef(b, k, n, 1, k), 0.0,
+                                        gk.MatMut.from_row_major(s, m, n))
+                else:
+                    gk.gemm(0.75, gk.MatRef.from_row_major(az, m, k), gk.MatRef(b, k, n, 1, k),
+                            0.0, gk.MatMut.from_row_major(s, m, n))
+                got = c[z * cbs:z * cbs + m * n]
+                assert torch.equal(got.view(torch.int16) if out == torch.bfloat16 else got,
+                                   s.view(torch.int16) if out == torch.bfloat16 else s), (name, z)
+                assert (c[z * cbs + m * n:(z + 1) * cbs] == 0).all()
