@@ -6,8 +6,8 @@
 // barrier per stage, the staged epilogue), with 16x16 blocks: on this chip
 // the 16x16 instructions draw less power per operation than the 32x32 ones,
 // so under the same power limit the clock stays higher (int8 16x16x64:
-// 4.2 POP/s sustained on back-to-back MFMAs at ~2.2 GHz, against 3.5 POP/s at
-// ~1.77 GHz for 32x32x32).  This file is built with the accumulators in
+// 4.29 POP/s sustained on back-to-back MFMAs at 2.14 GHz, against 3.5 POP/s
+// at 1.74 GHz for 32x32x32).  This file is built with the accumulators in
 // VGPRs (-mllvm -amdgpu-mfma-vgpr-form): with them in AGPRs the compiler
 // moves every 16x16 accumulator between register files around each MFMA.
 //
