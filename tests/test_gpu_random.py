@@ -169,3 +169,80 @@ def test_batched_random(dev, i, m, k, n, la, lb, lc, s, dt):
             gk.gemm_bf16_f32out(1.0, gk.MatRef(az, m, k, rsa, csa), gk.MatRef(bz, k, n, rsb, csb),
                                 0.0, gk.MatMut.from_row_major(one, m, n))
         assert torch.equal(c[z * m * n:(z + 1) * m * n], one), f"case {i} element {z}"
+
+
+def large_cases(seed, n):
+    """Big-tile shapes: sides across the 256-tile and one-round boundaries
+    (the 16x16-MFMA tile, the 352/384-wide one-round plans, the tail split),
+    K across the 128-byte stage edges."""
+    rng = np.random.default_rng(seed)
+    sides = [1024, 2047, 2048, 2049, 2816, 3000, 4096, 4100]
+    ks = [128, 200, 1000, 2048, 4096, 4100]
+    out = []
+    for i in range(n):
+        m = int(rng.choice(sides)) if rng.random() < 0.6 else int(rng.integers(1000, 4200))
+        nn = int(rng.choice(sides)) if rng.random() < 0.6 else int(rng.integers(1000, 4200))
+        k = int(rng.choice(ks)) if rng.random() < 0.6 else int(rng.integers(128, 4200))
+        la, lb, lc = (str(rng.choice(LAYOUTS)) for _ in range(3))
+        out.append((i, m, k, nn, la, lb, lc, int(rng.integers(0, 1 << 30))))
+    return out
+
+
+@pytest.mark.parametrize("i,m,k,n,la,lb,lc,s", large_cases(0xF66, 10))
+def test_i8_large_random(dev, i, m, k, n, la, lb, lc, s):
+    """Every element against the CPU port of gemmkit's i8 path (pinned
+    bit-exact to the oracle's closed form in test_oracle.py)."""
+    rng = np.random.default_rng(s)
+    a = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    c0 = rng.integers(-1000, 1000, (m, n), dtype=np.int32)
+    alpha, beta = int(rng.choice([1, 3, -2])), int(rng.choice([0, 1, -1]))
+    rsa, csa, al = layout_strides(m, k, la, 16)
+    rsb, csb, bl = layout_strides(k, n, lb, 16)
+    rsc, csc, cl = layout_strides(m, n, lc, 4)
+    abuf, bbuf = scatter(a, rsa, csa, al), scatter(b, rsb, csb, bl)
+    cbuf = scatter(c0, rsc, csc, cl, fill=-77)
+    want = cbuf.copy()
+    oracle.port_gemm_i8(m, k, n, alpha, abuf, rsa, csa, bbuf, rsb, csb, beta, want, rsc, csc)
+    cd = to_dev(cbuf, dev)
+    gk.gemm_i8(alpha, gk.MatRef(to_dev(abuf, dev), m, k, rsa, csa),
+               gk.MatRef(to_dev(bbuf, dev), k, n, rsb, csb), beta, gk.MatMut(cd, m, n, rsc, csc))
+    got = cd.cpu().numpy()
+    bad = np.flatnonzero(got != want)
+    assert bad.size == 0, f"case {i}: {m}x{k}x{n} {la}/{lb}/{lc}: {bad.size} elements differ"
+
+
+@pytest.mark.parametrize("i,m,k,n,la,lb,lc,s", large_cases(0xF77, 6))
+def test_requant_large_random(dev, i, m, k, n, la, lb, lc, s):
+    """Requantized big-tile products, every byte against the CPU port's
+    requantizing path."""
+    import torch
+    rng = np.random.default_rng(s)
+    a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-127, 128, (k, n), dtype=np.int8)
+    rsa, csa, al = layout_strides(m, k, la, 16)
+    rsb, csb, bl = layout_strides(k, n, lb, 16)
+    rsc, csc, cl = layout_strides(m, n, lc, 4)
+    abuf, bbuf = scatter(a, rsa, csa, al), scatter(b, rsb, csb, bl)
+    axis = int(rng.integers(0, 2))
+    ch = n if axis else m
+    scales = (1e-4 + rng.random(ch) * (1e-2 - 1e-4)).astype(np.float32)
+    bias = rng.integers(-65536, 65537, ch, dtype=np.int32)
+    u8 = bool(rng.random() < 0.4)
+    zp = int(rng.integers(0, 256)) if u8 else int(rng.integers(-128, 128))
+    relu = bool(rng.random() < 0.5)
+    lo, hi = (0, 255) if u8 else (-128, 127)
+    lo_eff = max(lo, zp) if relu else lo
+    want = np.zeros(cl, np.uint8)
+    oracle.port_gemm_i8_requant(m, k, n, abuf, rsa, csa, bbuf, rsb, csb, 0.0, scales, zp, bias,
+                                axis, lo_eff, hi, want, rsc, csc)
+    cd = torch.zeros(cl, dtype=torch.uint8 if u8 else torch.int8, device=dev)
+    sd = to_dev(scales, dev)
+    req = gk.Requantize(gk.RequantScale.PerCol(sd) if axis else gk.RequantScale.PerRow(sd), zp,
+                        to_dev(bias, dev), bias_axis="col" if axis else "row", relu=relu)
+    (gk.gemm_i8_requant_u8 if u8 else gk.gemm_i8_requant)(
+        gk.MatRef(to_dev(abuf, dev), m, k, rsa, csa), gk.MatRef(to_dev(bbuf, dev), k, n, rsb, csb),
+        req, gk.MatMut(cd, m, n, rsc, csc))
+    got = cd.cpu().numpy().view(np.uint8)
+    bad = np.flatnonzero(got != want)
+    assert bad.size == 0, f"case {i}: {m}x{k}x{n} {la}/{lb}/{lc} axis={axis} u8={u8}: {bad.size} differ"

@@ -305,6 +305,39 @@ def test_cpu_port_bit_exact(m, k, n, alpha, beta, row_major_c):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("la,lb,lc", [("row", "col", "row"), ("col", "row", "col"),
+                                      ("row+", "col+", "col+"), ("col+", "row+", "row")])
+def test_cpu_port_strided_layouts(la, lb, lc):
+    """The port from any operand strides (it packs them, as gemmkit does),
+    i32 and requantized, against the closed forms: the GPU tests check large
+    strided products against it."""
+    from helpers import layout_strides, scatter
+    rng = np.random.default_rng(0x5EED)
+    for m, k, n in [(37, 53, 29), (64, 130, 70), (5, 300, 17)]:
+        a = rng.integers(-128, 128, (m, k), dtype=np.int8)
+        b = rng.integers(-128, 128, (k, n), dtype=np.int8)
+        c0 = rng.integers(-1000, 1000, (m, n), dtype=np.int32)
+        rsa, csa, al = layout_strides(m, k, la, 16)
+        rsb, csb, bl = layout_strides(k, n, lb, 16)
+        rsc, csc, cl = layout_strides(m, n, lc, 4)
+        ab, bb = scatter(a, rsa, csa, al), scatter(b, rsb, csb, bl)
+        cb = scatter(c0, rsc, csc, cl, fill=-77)
+        want, got = cb.copy(), cb.copy()
+        oracle.gemm_i8(m, k, n, 3, ab, rsa, csa, bb, rsb, csb, -1, want, rsc, csc)
+        oracle.port_gemm_i8(m, k, n, 3, ab, rsa, csa, bb, rsb, csb, -1, got, rsc, csc, threads=2)
+        assert np.array_equal(got, want)
+        for axis in (0, 1):
+            ch = n if axis else m
+            sc = (1e-4 + rng.random(ch) * 1e-2).astype(np.float32)
+            bias = rng.integers(-65536, 65537, ch, dtype=np.int32)
+            q_want, q_got = np.zeros(cl, np.uint8), np.zeros(cl, np.uint8)
+            oracle.gemm_i8_requant(m, k, n, ab, rsa, csa, bb, rsb, csb, 0.0, sc, 5, bias, axis,
+                                   5, 127, q_want, rsc, csc)
+            oracle.port_gemm_i8_requant(m, k, n, ab, rsa, csa, bb, rsb, csb, 0.0, sc, 5, bias,
+                                        axis, 5, 127, q_got, rsc, csc, threads=2)
+            assert np.array_equal(q_got, q_want)
+
+
 def test_generators_are_reproducible():
     assert oracle.rng_next_u64(7, 3) == oracle.rng_next_u64(7, 3)
     x = oracle.rng_i8_full(5, 100000)
