@@ -246,3 +246,33 @@ def test_requant_large_random(dev, i, m, k, n, la, lb, lc, s):
     got = cd.cpu().numpy().view(np.uint8)
     bad = np.flatnonzero(got != want)
     assert bad.size == 0, f"case {i}: {m}x{k}x{n} {la}/{lb}/{lc} axis={axis} u8={u8}: {bad.size} differ"
+
+
+@pytest.mark.parametrize("i,m,k,n,la,lb,lc,s", large_cases(0xF88, 4))
+@pytest.mark.parametrize("out", ["f32", "bf16"])
+def test_bf16_large_random(dev, i, m, k, n, la, lb, lc, s, out):
+    """Big-tile bf16 products (the 16x16-MFMA tile and the one-round plans)
+    against the f64 product of the bf16-rounded inputs (numpy's f64 matmul: the
+    closed form at this size), elementwise within the bf16 bar."""
+    rng = np.random.default_rng(s)
+    abits = oracle.bf16_bits(rng.standard_normal(m * k).astype(np.float32))
+    bbits = oracle.bf16_bits(rng.standard_normal(k * n).astype(np.float32))
+    af = oracle.bf16_to_f32(abits).reshape(m, k).astype(np.float64)
+    bf = oracle.bf16_to_f32(bbits).reshape(k, n).astype(np.float64)
+    rsa, csa, al = layout_strides(m, k, la, 8)
+    rsb, csb, bl = layout_strides(k, n, lb, 8)
+    abuf = scatter(abits.reshape(m, k), rsa, csa, al)
+    bbuf = scatter(bbits.reshape(k, n), rsb, csb, bl)
+    ref = af @ bf
+    A = gk.MatRef(bf16_tensor_from_bits(abuf, dev), m, k, rsa, csa)
+    B = gk.MatRef(bf16_tensor_from_bits(bbuf, dev), k, n, rsb, csb)
+    if out == "f32":
+        c = torch.empty(m * n, dtype=torch.float32, device=dev)
+        gk.gemm_bf16_f32out(1.0, A, B, 0.0, gk.MatMut.from_row_major(c, m, n))
+    else:
+        c = torch.empty(m * n, dtype=torch.bfloat16, device=dev)
+        gk.gemm(1.0, A, B, 0.0, gk.MatMut.from_row_major(c, m, n))
+    got = c.float().cpu().numpy().reshape(m, n).astype(np.float64)
+    floor = 1e-3 * np.abs(ref).max()
+    ok = np.abs(got - ref) <= 1e-2 * np.maximum(np.abs(ref), floor)
+    assert ok.all(), f"case {i}: {m}x{k}x{n} {la}/{lb} {out}: {np.count_nonzero(~ok)} elements off"
