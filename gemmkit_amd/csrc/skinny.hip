@@ -168,9 +168,12 @@ __global__ __launch_bounds__(kSkThreads) void skinny_mfma(const GemvArgs g, cons
         for (int p = 0; p < kSkPF; ++p) {
             const int s = s0 + p;
             const bool in = live && s < ks1 && (int64_t)s * kSkStep + 16 * chunk < kb;
-            // Out-of-range lanes get bit 31 set (past any resource size here),
-            // without a select: every load is issued on every path, so the
-            // wait counts after a batch are exact.
+            // Out-of-range lanes get bit 31 set, past any resource size here
+            // (an item spans at most 32 rows of at most 8 MiB, both for the
+            // matrix's row stride and its row, so num and every in-range
+            // offset stay below 2^31), without a select: every load is
+            // issued on every path, so the wait counts after a batch are
+            // exact.
             const uint32_t oor = (uint32_t)!in << 31;
 #pragma unroll
             for (int b = 0; b < BLK; ++b)
