@@ -99,16 +99,17 @@ _KIND_CODES = {"i32": 0, "f32": 1, "bf16": 2, "q8": 3}
 
 
 def debug_plan(in_type: str, kind: str, m: int, n: int, kbytes: int, batch: int = 1,
-               pitches: bool = False):
+               pitches: bool = False, ld_b: int = 0):
     """Extension (no reference counterpart): the matrix-core launch plan the
     dispatcher would choose for an m x n product in the kernel frame with
-    `kbytes` bytes of K per row, as (tile, na, tile_b): na > 0 means a second
-    launch covers columns [na, n) with tile_b.  pitches=True: (tile, pitch,
-    na, tile_b, pitch_b), a pitch of 0 meaning the tile's width.  Host-only."""
+    `kbytes` bytes of K per row (and B^T rows `ld_b` bytes apart, 0 for
+    packed rows), as (tile, na, tile_b): na > 0 means a second launch covers
+    columns [na, n) with tile_b.  pitches=True: (tile, pitch, na, tile_b,
+    pitch_b), a pitch of 0 meaning the tile's width.  Host-only."""
     t, na, tb = C.c_int32(), C.c_int64(), C.c_int32()
     pa, pb = C.c_int32(), C.c_int32()
     _check(_lib.lib().gk_debug_plan(_IN_CODES[in_type], _KIND_CODES[kind], m, n, batch, kbytes,
-                                    C.byref(t), C.byref(na), C.byref(tb), C.byref(pa),
+                                    ld_b, C.byref(t), C.byref(na), C.byref(tb), C.byref(pa),
                                     C.byref(pb)))
     if pitches:
         return TILE_NAMES[t.value], pa.value, na.value, TILE_NAMES[tb.value], pb.value

@@ -82,7 +82,7 @@ SIGNATURES: dict[str, tuple] = {
     "gk_last_error": (C.c_char_p, []),
     "gk_version": (C.c_char_p, []),
     "gk_debug_plan": (C.c_int, [C.c_int32, C.c_int32, C.c_int64, C.c_int64, C.c_int64, C.c_int64,
-                                C.POINTER(C.c_int32), C.POINTER(C.c_int64),
+                                C.c_int64, C.POINTER(C.c_int32), C.POINTER(C.c_int64),
                                 C.POINTER(C.c_int32), C.POINTER(C.c_int32),
                                 C.POINTER(C.c_int32)]),
     "gk_debug_mfma_ceiling": (C.c_int, [C.c_int32, C.c_int64, C.c_int32, C.c_int32,

@@ -570,15 +570,16 @@ bool m16_allowed(InType in, int64_t kbytes) {
     return in == InType::I8 || kbytes > kstream_max_kbytes();
 }
 
+// m16: whether the 16x16-MFMA tile may be picked (on top of m16_allowed).
 Tile pick_tile(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind kind, InType in,
-               double *cost_out = nullptr) {
+               double *cost_out = nullptr, bool m16 = true) {
     bool forced;
     Tile t = env_tile(&forced);
     if (forced) return t;
     double best = 1e300;
     Tile bt = Tile::T64x64;
     for (const TileCand &c : kTileCands) {
-        if (c.t == Tile::T256x256w8m16 && !m16_allowed(in, kbytes)) continue;
+        if (c.t == Tile::T256x256w8m16 && (!m16 || !m16_allowed(in, kbytes))) continue;
         const double cost = tile_cost(c, M, N, batch, kbytes, kind, in);
         if (cost < best * 0.999) { best = cost; bt = c.t; }
     }
@@ -661,14 +662,36 @@ bool plan_tail_split(int64_t M, int64_t N, int64_t kbytes, EpiKind kind, InType 
 // na < N, tile `tb` over [na, N) at pitch pn_b.
 struct MmaPlan { Tile ta; int32_t pn_a; int64_t na; Tile tb; int32_t pn_b; };
 
-MmaPlan plan_mma(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind kind, InType in) {
+// ld_b: B^T's row stride in bytes.  The wide and strip tiles address 384 and
+// 352 rows of B^T with 32-bit offsets from the panel's first row, so they are
+// taken only when those rows plus the K bytes stay below 2^31 (the 256-row
+// tiles are covered by the stride limit the caller enforces by packing).
+bool wide_fits(const TileCand &c, int64_t ld_b, int64_t kbytes) {
+    return panels_fit(1, c.bn, 0, ld_b, kbytes);
+}
+
+MmaPlan plan_mma(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind kind, InType in,
+                 int64_t ld_b = 0) {
     bool forced;
     env_tile(&forced);
     double cost = 0.0;
-    const Tile t = pick_tile(M, N, batch, kbytes, kind, in, &cost);
+    // bf16 sums in the 16x16-MFMA tile's order differ in the last bits from
+    // the 32x32 tiles' (all of which share one order), so a batch takes the
+    // family its element's standalone plan takes: the 16x16 tile exactly
+    // when that plan is the 16x16 tile, otherwise the best 32x32 tile for the
+    // batch.  Every batched element then equals its standalone call bit for
+    // bit (src/api/batched.rs:172-176).  int8 sums are exact in any order.
+    bool m16 = true;
+    if (in == InType::BF16 && batch > 1 && !forced) {
+        const MmaPlan one = plan_mma(M, N, 1, kbytes, kind, in, ld_b);
+        if (one.ta == Tile::T256x256w8m16) return MmaPlan{one.ta, 0, N, one.ta, 0};
+        m16 = false;
+    }
+    const Tile t = pick_tile(M, N, batch, kbytes, kind, in, &cost, m16);
     if (forced) {
         int32_t p = 0;
         if (batch == 1 && (t == kRoundWide.t || t == kRoundStrip.t)) p = rest_pitch(tile_cand(t), M, N);
+        // (a forced wide tile whose rows do not fit is refused at launch)
         return MmaPlan{t, p, N, t, 0};
     }
     MmaPlan plan{t, 0, N, t, 0};
@@ -684,6 +707,7 @@ MmaPlan plan_mma(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind ki
     if (batch == 1 && in != InType::F32 && wide_round_enabled()) {
         for (const TileCand *c : {&kRoundStrip, &kRoundWide}) {
             if (c == &kRoundStrip && in != InType::I8) continue;
+            if (!wide_fits(*c, ld_b, kbytes)) continue;
             const int32_t p = rest_pitch(*c, M, N);
             if (p <= 256) continue;
             if (p * 100 >= c->bn * 85) {
@@ -1099,7 +1123,7 @@ int run_fit(const Region &rg, InType in, EpiParams ep, int64_t m, int64_t k, int
         if (e != hipSuccess) return hip_fail(e, "kstream launch");
         return finish("mfma gemm (short K)");
     }
-    const MmaPlan plan = plan_mma(M, N, batch, kbytes, ep.kind, in);
+    const MmaPlan plan = plan_mma(M, N, batch, kbytes, ep.kind, in, Bt.rs * (int64_t)esz);
     if (plan.na < N) {
         // Tail split: kernel-frame columns [0, na) with the first tile,
         // [na, N) with the rest's (at its column pitch, if any): B^T rows, C
@@ -1902,11 +1926,13 @@ const char *gk_last_error(void) { return tl_error.c_str(); }
 const char *gk_version(void) { return "gemmkit-hip 0.1.0 (gfx950)"; }
 
 int gk_debug_plan(int32_t in, int32_t kind, int64_t m, int64_t n, int64_t batch, int64_t kbytes,
-                  int32_t *tile, int64_t *na, int32_t *tile_b, int32_t *pn_a, int32_t *pn_b) {
+                  int64_t ld_b, int32_t *tile, int64_t *na, int32_t *tile_b, int32_t *pn_a,
+                  int32_t *pn_b) {
     if (in < 0 || in > 2 || kind < 0 || kind > 3 || m <= 0 || n <= 0 || batch <= 0 ||
-        kbytes < 0 || !tile || !na || !tile_b)
+        kbytes < 0 || ld_b < 0 || !tile || !na || !tile_b)
         return fail(GK_ERR_ARG, "gemmkit: gk_debug_plan: bad argument");
-    const MmaPlan plan = plan_mma(m, n, batch, kbytes, (EpiKind)kind, (InType)in);
+    if (ld_b == 0) ld_b = (kbytes + 15) / 16 * 16;
+    const MmaPlan plan = plan_mma(m, n, batch, kbytes, (EpiKind)kind, (InType)in, ld_b);
     *tile = (int32_t)plan.ta;
     *na = plan.na < n ? plan.na : 0;
     *tile_b = (int32_t)plan.tb;

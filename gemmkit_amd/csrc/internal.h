@@ -53,6 +53,20 @@ enum FusedAct : int32_t { kActNone = 0, kActRelu = 1, kActLeakyRelu = 2 };
 // address: 256 row strides plus a row stay below 2^31 bytes of 32-bit buffer
 // offsets.
 constexpr int64_t kMaxTileRowBytes = 0x7FFFFFF0 / 256;
+// Buffer-resource sizes of the matrix-core kernels stay at or below
+// kMaxRecords; a lane meant to read zeros uses the offset kOutOfRange.  Every
+// row a tile addresses (all BM rows of A and BN rows of B^T, past the matrix
+// edge and the column pitch included) plus its K bytes must stay within
+// kMaxRecords, so 32-bit offsets never wrap and kOutOfRange is always out of
+// range.
+constexpr uint32_t kMaxRecords = 0x7FFFFFF0u;
+constexpr uint32_t kOutOfRange = 0x80000000u;
+static_assert(kOutOfRange > kMaxRecords, "out-of-range offset must exceed every resource size");
+inline bool panels_fit(int64_t bm, int64_t bn, int64_t lda_bytes, int64_t ldb_bytes, int64_t kbytes) {
+    const int64_t kb16 = (kbytes + 15) / 16 * 16;
+    return (bm - 1) * lda_bytes + kb16 <= (int64_t)kMaxRecords &&
+           (bn - 1) * ldb_bytes + kb16 <= (int64_t)kMaxRecords;
+}
 
 struct MmaArgs {
     const void *a;         // M x K, k-contiguous

@@ -449,6 +449,9 @@ hipError_t launch_mfma16_ceiling(InType in, int blocks, int64_t iters, uint32_t 
 template <InType T, EpiKind E>
 static hipError_t launch16(const MmaArgs &args, const EpiParams &ep, hipStream_t stream) {
     if ((args.pn != 0 && args.pn != 256) || args.splits > 1) return hipErrorInvalidValue;
+    const int esz = T == InType::I8 ? 1 : 2;
+    if (!panels_fit(256, 256, args.lda * esz, args.ldb * esz, (int64_t)args.K * esz))
+        return hipErrorInvalidValue;
     const int tiles = ((args.M + 255) / 256) * ((args.N + 255) / 256);
     hipLaunchKernelGGL((mma16_kernel<T, E>), dim3(tiles, 1, args.batch), dim3(512), 0, stream,
                        args, ep);

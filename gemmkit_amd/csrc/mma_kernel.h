@@ -115,10 +115,8 @@ constexpr int kSchedVmem = 0x010;
 // resource's size reads zeros and touches no memory.  That zero-fills the rows
 // past the matrix edge and the K tail of the last stage, and lets the loop
 // issue its loads past the end of K without traffic.  Offsets stay below
-// kMaxRecords, which the host guarantees for every in-range byte of a tile.
-constexpr uint32_t kMaxRecords = 0x7FFFFFF0u;
-constexpr uint32_t kOutOfRange = 0x80000000u;
-static_assert(kOutOfRange > kMaxRecords, "out-of-range offset must exceed every resource size");
+// kMaxRecords (internal.h), which the host guarantees for every row a tile
+// addresses.
 constexpr int kRsrcWord3 = 0x00020000;  // raw (unswizzled) buffer, 32-bit data format
 
 // One direct-to-LDS load of 16 bytes per lane: lane l reads base[voff] into
@@ -949,6 +947,10 @@ template <InType T, EpiKind E, int BM, int BN, int WM, int WN, int NS, bool SPLI
 static hipError_t launch_one(const MmaArgs &args, const EpiParams &ep, hipStream_t stream) {
     const int pn = args.pn > 0 ? args.pn : BN;
     if (pn > BN || pn % 4 != 0) return hipErrorInvalidValue;
+    const int esz = T == InType::I8 ? 1 : (T == InType::BF16 ? 2 : 4);
+    if (!panels_fit(BM, BN, args.lda * esz, args.ldb * esz,
+                    (int64_t)(SPLIT ? args.kchunk : args.K) * esz))
+        return hipErrorInvalidValue;
     int tiles = ((args.M + BM - 1) / BM) * ((args.N + pn - 1) / pn);
     dim3 grid(tiles, SPLIT ? args.splits : 1, args.batch);
     hipLaunchKernelGGL((mma_kernel<T, E, BM, BN, WM, WN, BK, NS, SPLIT>), grid,

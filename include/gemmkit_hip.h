@@ -53,7 +53,8 @@ const char *gk_version(void);
 
 /* Launch plan of the matrix-core route for a product in the kernel frame (M x N
  * output, K bytes per operand row; in: 0 int8, 1 bf16, 2 f32; kind: 0 i32,
- * 1 f32, 2 bf16, 3 requantized i8/u8 output), as the dispatcher would choose
+ * 1 f32, 2 bf16, 3 requantized i8/u8 output; ld_b: B^T's row stride in bytes,
+ * 0 for rows of K bytes rounded up to 16), as the dispatcher would choose
  * it with the current environment: *tile is the tile of the (first) launch,
  * *na the kernel-frame columns it covers when the product is split into two
  * launches (else 0), *tile_b the tile of the second launch, *pn_a and *pn_b
@@ -61,7 +62,8 @@ const char *gk_version(void);
  * width).  Host-only, no device needed.  No counterpart in the reference: it
  * exposes the tile choice to tests and tuning tools. */
 int gk_debug_plan(int32_t in, int32_t kind, int64_t m, int64_t n, int64_t batch, int64_t kbytes,
-                  int32_t *tile, int64_t *na, int32_t *tile_b, int32_t *pn_a, int32_t *pn_b);
+                  int64_t ld_b, int32_t *tile, int64_t *na, int32_t *tile_b, int32_t *pn_a,
+                  int32_t *pn_b);
 
 /* Diagnostics with no counterpart in the reference: the ceilings the kernels
  * are measured against.

@@ -145,3 +145,35 @@ def test_forced_wide_tile_takes_the_round_pitch(clean_env, monkeypatch):
 def test_bad_arguments():
     with pytest.raises(gk.GemmkitError):
         gk.debug_plan("i8", "i32", 0, 16, 16)
+
+
+# bf16: the 16x16-MFMA tile sums in another order than the 32x32 tiles, so a
+# batch must take the tile family its element's standalone plan takes, or a
+# batched element would differ from its standalone call in the last bits
+# (src/api/batched.rs:172-176).  Every shape x K x batch of this grid.
+@pytest.mark.parametrize("kind", ["f32", "bf16"])
+def test_bf16_batch_takes_the_standalone_tile_family(clean_env, kind):
+    sides = [256, 512, 768, 1024, 1536, 2048, 3072, 4096]
+    bad = []
+    for m in sides:
+        for n in sides:
+            for kbytes in (512, 1024, 4096, 8192):
+                one = gk.debug_plan("bf16", kind, m, n, kbytes, 1)[0] == "256x256w8m16"
+                for batch in (2, 4, 8, 16, 64):
+                    many = gk.debug_plan("bf16", kind, m, n, kbytes, batch)[0] == "256x256w8m16"
+                    if many != one:
+                        bad.append((m, n, kbytes, batch, one, many))
+    assert not bad, bad[:5]
+
+
+def test_wide_tiles_keep_their_rows_within_32bit_offsets(clean_env):
+    # 8192 x 2640 int8 products take the one-round strip tile (pitch 336) with
+    # packed rows; with B^T rows 8 MB apart its 352 rows would span 2.8 GB of
+    # 32-bit buffer offsets, so the plan must not take the wide tiles then.
+    assert gk.debug_plan("i8", "i32", 8192, 2640, 4112, pitches=True)[0] == "256x352w8k128"
+    for ld in (8000016, 6 << 20):
+        t = gk.debug_plan("i8", "i32", 8192, 2640, 4112, ld_b=ld)[0]
+        assert t not in ("256x352w8k128", "256x384w8k128"), (ld, t)
+    # the largest stride that still fits keeps it
+    ld_max = (0x7FFFFFF0 - 4112) // 351
+    assert gk.debug_plan("i8", "i32", 8192, 2640, 4112, ld_b=ld_max)[0] == "256x352w8k128"
