@@ -583,59 +583,6 @@ def run_extras(args, workloads, want, timed, dev, gk, np, torch, traffic_all, or
         workloads["packed_small_m"] = res
         del bf, pf, bi, pi
 
-    # the HBM read ceiling at the matrix-vector sizes: a plain read of the
-    # 14336 x 4096 int8 weight (ROTATE copies, as the GEMV workloads cycle)
-    # and of a 1 GiB buffer, at 1-8 workgroups per CU (not in the default run)
-    if args.only == "hbm_read":
-        import ctypes
-        from gemmkit_amd import _lib
-        lib = _lib.lib()
-        sink = torch.empty(256 * 64, dtype=torch.int32, device=dev)
-        res = {}
-        for label, nbytes, count in (("w_14336x4096", 14336 * 4096, ROTATE),
-                                     ("buf_1gib", 1 << 30, 1)):
-            bufs = [torch.randint(-127, 128, (nbytes,), dtype=torch.int8, device=dev)
-                    for _ in range(count)]
-            for wgs in (1, 2, 3, 4, 8):
-                def call(b, wgs=wgs, nbytes=nbytes):
-                    rc = lib.gk_debug_read_stream(ctypes.c_void_p(b.data_ptr()), nbytes, wgs,
-                                                  ctypes.c_void_p(sink.data_ptr()),
-                                                  ctypes.c_void_p(torch.cuda.current_stream()
-                                                                  .cuda_stream))
-                    if rc != 0:
-                        raise RuntimeError(f"gk_debug_read_stream failed: {rc}")
-                ms = timed([lambda b=b: call(b) for b in bufs], 10 * count, warm)
-                res[f"{label}_wg{wgs}"] = {"us": ms * 1e3, **timed.last, "GBps": nbytes / ms / 1e6,
-                                           "frac_hbm": nbytes / (ms * 1e-3) / PEAK["hbm"]}
-            del bufs
-        workloads["hbm_read"] = res
-
-    # the HBM write ceiling at the attention-score output size (64 x 512 x 512
-    # f32, ROTATE buffers) and over 1 GiB, nontemporal and cached stores
-    # (not in the default run)
-    if args.only == "hbm_write":
-        import ctypes
-        from gemmkit_amd import _lib
-        lib = _lib.lib()
-        res = {}
-        for label, nbytes, count in (("scores_64x512x512_f32", 64 * 512 * 512 * 4, ROTATE),
-                                     ("buf_1gib", 1 << 30, 1)):
-            bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(count)]
-            for nt in (1, 0):
-                for wgs in (1, 2, 4, 8):
-                    def call(b, wgs=wgs, nbytes=nbytes, nt=nt):
-                        rc = lib.gk_debug_write_stream(
-                            ctypes.c_void_p(b.data_ptr()), nbytes, wgs, nt,
-                            ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
-                        if rc != 0:
-                            raise RuntimeError(f"gk_debug_write_stream failed: {rc}")
-                    ms = timed([lambda b=b: call(b) for b in bufs], 10 * count, warm)
-                    res[f"{label}_{'nt' if nt else 'cached'}_wg{wgs}"] = {
-                        "us": ms * 1e3, **timed.last, "GBps": nbytes / ms / 1e6,
-                        "frac_hbm": nbytes / (ms * 1e-3) / PEAK["hbm"]}
-            del bufs
-        workloads["hbm_write"] = res
-
     # a plain elementwise kernel over 1 GiB in, 1 GiB out (reads and writes
     # each byte once): the calibration workload for the HBM byte counters
     if args.only == "copy_1gib":

@@ -85,10 +85,6 @@ SIGNATURES: dict[str, tuple] = {
                                 C.c_int64, C.POINTER(C.c_int32), C.POINTER(C.c_int64),
                                 C.POINTER(C.c_int32), C.POINTER(C.c_int32),
                                 C.POINTER(C.c_int32)]),
-    "gk_debug_mfma_ceiling": (C.c_int, [C.c_int32, C.c_int64, C.c_int32, C.c_int32,
-                                        C.POINTER(C.c_double), C.POINTER(C.c_double)]),
-    "gk_debug_read_stream": (C.c_int, [_vp, C.c_int64, C.c_int32, _vp, _vp]),
-    "gk_debug_write_stream": (C.c_int, [_vp, C.c_int64, C.c_int32, C.c_int32, _vp]),
     "gk_init": (C.c_int, []),
     "gk_set_stream": (C.c_int, [_vp]),
     "gk_get_stream": (_vp, []),

@@ -470,7 +470,7 @@ static bool gemv_beats_skinny(InType in, int64_t short_side, int64_t kbytes) {
 // the arithmetic sooner), plus a fixed per-tile latency (first stages in
 // flight).  A fraction `hide` of the epilogue and latency overlaps the next
 // tile's main loop when a CU runs more than one; the last is never hidden.
-// The constants are the fit of gemmkit_amd/calibrate_tiles.py to graph-timed
+// The constants are the fit of a tile sweep (profiles/tile_choice.md) to graph-timed
 // runs of 17 shapes x 8 tiles (int8 i32 and requantized, bf16 with f32 and
 // bf16 output, batched attention scores, f32; 1024^2 to 4096^3 and
 // 2048 x 11008 x 4096): least squares on log time, then refined so the chosen

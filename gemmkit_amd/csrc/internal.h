@@ -110,9 +110,6 @@ hipError_t launch_mma(InType in, Tile tile, const MmaArgs &args, const EpiParams
 // The 256 x 256 tile on 16x16 matrix-core instructions (mma16.hip): int8
 // (i32, requantized) and bf16 (f32, bf16) output, unsplit, unpitched.
 hipError_t launch_mma16(InType in, const MmaArgs &args, const EpiParams &ep, hipStream_t stream);
-// The ceiling probe's 16x16 variant (mma16.hip, built like the tile).
-hipError_t launch_mfma16_ceiling(InType in, int blocks, int64_t iters, uint32_t *sink,
-                                 uint64_t *clocks);
 
 // Short-contraction route (kstream.hip): K*esz <= kstream_max_kbytes(), the
 // same kernel frame and bit-identical results as launch_mma, 128-row panels

@@ -379,73 +379,6 @@ void mma16_kernel(const MmaArgs args, const EpiParams ep) {
     }
 }
 
-// Ceiling probe on the 16x16 instructions (gk_debug_mfma_ceiling, in = 2 and
-// 3): as mfma_ceiling_kernel in ceiling.hip, each wave keeping 32 independent
-// 16x16 accumulator blocks (128 registers, as a wave of the 16x16 tile) and
-// running `iters` rounds of 32 MFMAs on operands refreshed every round.
-template <InType T>
-__global__ __launch_bounds__(256) void mfma16_ceiling_kernel(int64_t iters, uint32_t *sink,
-                                                             uint64_t *clocks) {
-    using M = Mma16x<T>;
-    using acc_t = typename M::acc_t;
-    uint32_t s = 0x9E3779B9u ^ (blockIdx.x * 256u + threadIdx.x) * 0x85EBCA6Bu;
-    auto rnd = [&]() {
-        s ^= s << 13;
-        s ^= s >> 17;
-        s ^= s << 5;
-        return (int)s;
-    };
-    v4i a0 = {rnd(), rnd(), rnd(), rnd()}, a1 = {rnd(), rnd(), rnd(), rnd()};
-    v4i b0 = {rnd(), rnd(), rnd(), rnd()}, b1 = {rnd(), rnd(), rnd(), rnd()};
-    const int m = (int)0xBFFFBFFFu;  // bf16: keep operands finite
-    if constexpr (T == InType::BF16) {
-        a0 &= m; a1 &= m; b0 &= m; b1 &= m;
-    }
-    acc_t acc[32];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-        acc[i] = acc_t{};
-        acc[i][0] = (typename M::scalar_t)(i + 1);
-    }
-    uint64_t t0 = 0, r0 = 0;
-    const bool timer = blockIdx.x == 0 && threadIdx.x == 0;
-    if (timer) {
-        t0 = __builtin_amdgcn_s_memtime();
-        r0 = __builtin_amdgcn_s_memrealtime();
-    }
-    for (int64_t it = 0; it < iters; ++it) {
-#pragma unroll
-        for (int i = 0; i < 32; ++i)
-            acc[i] = M::step((i & 1) ? b1 : b0, (i & 2) ? a1 : a0, acc[i]);
-        a0 = a0 ^ (b1 << 1);
-        b0 = b0 ^ (a1 >> 1);
-        if constexpr (T == InType::BF16) {
-            a0 &= m; b0 &= m;
-        }
-    }
-    uint32_t fold = 0;
-#pragma unroll
-    for (int i = 0; i < 32; ++i)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) fold = fold * 31u + __builtin_bit_cast(uint32_t, acc[i][e]);
-    sink[blockIdx.x * 256 + threadIdx.x] = fold;
-    if (timer) {
-        clocks[0] = __builtin_amdgcn_s_memtime() - t0;
-        clocks[1] = __builtin_amdgcn_s_memrealtime() - r0;
-    }
-}
-
-hipError_t launch_mfma16_ceiling(InType in, int blocks, int64_t iters, uint32_t *sink,
-                                 uint64_t *clocks) {
-    if (in == InType::I8)
-        hipLaunchKernelGGL(mfma16_ceiling_kernel<InType::I8>, dim3(blocks), dim3(256), 0, nullptr,
-                           iters, sink, clocks);
-    else
-        hipLaunchKernelGGL(mfma16_ceiling_kernel<InType::BF16>, dim3(blocks), dim3(256), 0,
-                           nullptr, iters, sink, clocks);
-    return hipGetLastError();
-}
-
 template <InType T, EpiKind E>
 static hipError_t launch16(const MmaArgs &args, const EpiParams &ep, hipStream_t stream) {
     if ((args.pn != 0 && args.pn != 256) || args.splits > 1) return hipErrorInvalidValue;

@@ -65,35 +65,6 @@ int gk_debug_plan(int32_t in, int32_t kind, int64_t m, int64_t n, int64_t batch,
                   int64_t ld_b, int32_t *tile, int64_t *na, int32_t *tile_b, int32_t *pn_a,
                   int32_t *pn_b);
 
-/* Diagnostics with no counterpart in the reference: the ceilings the kernels
- * are measured against.
- *
- * gk_debug_mfma_ceiling: every CU issues back-to-back MFMAs on random
- * register operands (in: 0 int8 v_mfma_i32_32x32x32_i8, 1 bf16
- * v_mfma_f32_32x32x16_bf16, 16 per round into 16 32x32 blocks; 2 int8
- * v_mfma_i32_16x16x64_i8, 3 bf16 v_mfma_f32_16x16x32_bf16, 32 per round into
- * 32 16x16 blocks), `iters` rounds per wave, one 4-wave workgroup per CU
- * (wgs_per_cu must be 1: one wave per SIMD), `launches` launches of which the
- * last is timed (the ones before bring the clocks to their loaded state).
- * Returns the achieved rate (ops/s) and the shader clock the chip held (from
- * the shader and real-time counters): how far below the published peak the
- * power limit puts a GEMM kernel built on that instruction.
- *
- * gk_debug_read_stream: enqueues, on `stream`, one pass that reads `bytes`
- * (a multiple of 16, 16-byte aligned) from `buf` and writes next to nothing
- * (`sink` holds one 32-bit word per workgroup: cus * wgs_per_cu), the HBM
- * read ceiling for a matrix-vector product of the same size.
- *
- * gk_debug_write_stream: enqueues, on `stream`, one pass that writes `bytes`
- * (a multiple of 16, 16-byte aligned) of `buf`, with nontemporal stores when
- * `nontemporal` is nonzero: the HBM write ceiling. */
-int gk_debug_mfma_ceiling(int32_t in, int64_t iters, int32_t wgs_per_cu, int32_t launches,
-                          double *ops_per_s, double *clock_ghz);
-int gk_debug_read_stream(const void *buf, int64_t bytes, int32_t wgs_per_cu, void *sink,
-                         void *stream);
-int gk_debug_write_stream(void *buf, int64_t bytes, int32_t wgs_per_cu, int32_t nontemporal,
-                          void *stream);
-
 /* ---------------------------------------------------------------- runtime */
 
 /* Parallelism request (src/parallel.rs:25): 1 = Serial, 0 = Rayon(0) "all",

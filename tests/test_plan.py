@@ -3,7 +3,7 @@ cost model, the two-launch tail split and the one-round 256 x 384 plan at a
 column pitch, through gk_debug_plan.
 
 The expected tiles are the measured best forced tiles of the 17-shape sweep the
-model was fitted to (gemmkit_amd/calibrate_tiles.py), so a refit that loses one
+model was fitted to (profiles/tile_choice.md), so a refit that loses one
 of them fails here."""
 import os
 
