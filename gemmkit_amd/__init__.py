@@ -93,7 +93,7 @@ def version() -> str:
 TILE_NAMES = {0: "256x256", 1: "256x128", 2: "128x128", 3: "64x64", 4: "256x256w8",
               5: "256x128o2", 6: "256x256k128", 7: "256x256w8k128", 8: "128x192k128",
               9: "128x96k128o2", 10: "256x384w8k128",
-              11: "256x352w8k128", 12: "256x256w8m16"}
+              11: "256x352w8k128", 12: "256x256w8m16", 13: "256x352w8m16"}
 _IN_CODES = {"i8": 0, "bf16": 1, "f32": 2}
 _KIND_CODES = {"i32": 0, "f32": 1, "bf16": 2, "q8": 3}
 

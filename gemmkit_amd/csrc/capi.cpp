@@ -39,7 +39,20 @@ thread_local std::string tl_error;
 thread_local hipStream_t tl_stream = nullptr;
 thread_local int tl_sync = 1;
 
+// The workspace a call has taken (its event and recorded flag): the call's
+// end, or its failure after launching something, records the event on the
+// launch stream, which orders the arena's next user on another stream.
+thread_local hipEvent_t tl_ws_event = nullptr;
+thread_local bool *tl_ws_recorded = nullptr;
+
+void ws_mark_done() {
+    if (!tl_ws_recorded) return;
+    if (hipEventRecord(tl_ws_event, tl_stream) == hipSuccess) *tl_ws_recorded = true;
+    tl_ws_recorded = nullptr;
+}
+
 int fail(int code, const char *fmt, ...) {
+    ws_mark_done();
     char buf[1024];
     va_list ap;
     va_start(ap, fmt);
@@ -257,6 +270,12 @@ int validate_gemm_views(const gk_mat_ref *a, const gk_mat_ref *b, const gk_mat_m
 struct gk_workspace {
     void *ptr = nullptr;
     size_t bytes = 0;
+    // Ordering of the arena across streams (the reference's &mut Workspace
+    // has one user at a time, src/workspace.rs:53-60): the stream of the last
+    // call that used it and an event recorded after that call's launches.
+    hipStream_t last_stream = nullptr;
+    hipEvent_t done = nullptr;
+    bool recorded = false;
 };
 
 struct gk_packed_rhs {
@@ -279,15 +298,28 @@ namespace {
 // src/workspace.rs:205-230): created on first use and released when a worker
 // thread exits.  The main thread's arena is left to the process teardown,
 // where the HIP runtime may already be gone.
+// Waits until the arena's last user has finished with it (its event, not the
+// whole device: other threads' queued work is not waited for).
+void ws_quiesce(gk_workspace *ws) {
+    if (ws->recorded) (void)hipEventSynchronize(ws->done);
+    ws->recorded = false;
+}
+
+void ws_release(gk_workspace *ws) {
+    if (tl_ws_recorded == &ws->recorded) tl_ws_recorded = nullptr;
+    ws_quiesce(ws);
+    if (ws->ptr) (void)hipFree(ws->ptr);
+    ws->ptr = nullptr;
+    ws->bytes = 0;
+    if (ws->done) (void)hipEventDestroy(ws->done);
+    ws->done = nullptr;
+}
+
 struct ThreadWs {
     gk_workspace *ws = nullptr;
     ~ThreadWs() {
         if (!ws) return;
-        if (ws->ptr && (pid_t)syscall(SYS_gettid) != getpid()) {
-            (void)hipDeviceSynchronize();
-            (void)hipFree(ws->ptr);
-            ws->ptr = nullptr;
-        }
+        if ((pid_t)syscall(SYS_gettid) != getpid()) ws_release(ws);
         if (!ws->ptr) delete ws;
     }
 };
@@ -314,6 +346,7 @@ bool stream_capturing() {
 // reserves the arena beforehand (gk_workspace_with_capacity, or one eager call
 // of the same shape).
 int ws_reserve(gk_workspace *ws, size_t bytes, void **out) {
+    const bool capturing = stream_capturing();
     if (ws->bytes < bytes) {
         if (stream_capturing())
             return fail(GK_ERR_NOMEM,
@@ -324,9 +357,13 @@ int ws_reserve(gk_workspace *ws, size_t bytes, void **out) {
         size_t want = std::max(bytes, ws->bytes + ws->bytes / 2);
         want = (want + 0xFFFFF) & ~(size_t)0xFFFFF;
         if (ws->ptr) {
-            // Work already queued may still read the old arena.
-            hipError_t e = hipDeviceSynchronize();
-            if (e != hipSuccess) return hip_fail(e, "workspace grow");
+            // Work already queued may still read the old arena: wait for its
+            // last user.
+            if (ws->recorded) {
+                hipError_t e = hipEventSynchronize(ws->done);
+                if (e != hipSuccess) return hip_fail(e, "workspace grow");
+                ws->recorded = false;
+            }
             (void)hipFree(ws->ptr);
             ws->ptr = nullptr;
             ws->bytes = 0;
@@ -338,12 +375,30 @@ int ws_reserve(gk_workspace *ws, size_t bytes, void **out) {
         }
         ws->bytes = want;
     }
+    // A call on another stream than the arena's last user first waits for
+    // that user's work (its packs and partial sums live in the arena).
+    // Captured calls follow the graph's own ordering: nothing is waited for
+    // or recorded under capture.
+    if (!capturing) {
+        if (ws->recorded && ws->last_stream != tl_stream) {
+            hipError_t e = hipStreamWaitEvent(tl_stream, ws->done, 0);
+            if (e != hipSuccess) return hip_fail(e, "workspace stream order");
+        }
+        if (!ws->done) {
+            hipError_t e = hipEventCreateWithFlags(&ws->done, hipEventDisableTiming);
+            if (e != hipSuccess) return hip_fail(e, "workspace event");
+        }
+        ws->last_stream = tl_stream;
+        tl_ws_event = ws->done;
+        tl_ws_recorded = &ws->recorded;
+    }
     *out = ws->ptr;
     return GK_OK;
 }
 
 int finish(const char *what) {
     hipError_t e = hipGetLastError();
+    ws_mark_done();
     if (e != hipSuccess) return hip_fail(e, what);
     if (tl_sync) {
         e = hipStreamSynchronize(tl_stream);
@@ -422,6 +477,7 @@ Tile env_tile(bool *forced) {
     if (!strcmp(s, "256x384w8k128")) return Tile::T256x384w8k128;
     if (!strcmp(s, "256x352w8k128")) return Tile::T256x352w8k128;
     if (!strcmp(s, "256x256w8m16")) return Tile::T256x256w8m16;
+    if (!strcmp(s, "256x352w8m16")) return Tile::T256x352w8m16;
     *forced = false;
     return Tile::T256x256;
 }
@@ -524,6 +580,11 @@ static const TileCand kRoundWide = {Tile::T256x384w8k128, 256, 384, 1, {0.821426
 // bf16 layer), so bf16 keeps the 384-wide tile.
 static const TileCand kRoundStrip = {Tile::T256x352w8k128, 256, 352, 1, {0.821426, 0.821426},
                                      1.278928, 0.0, 0.992329, 0.969417};
+// The 256 x 352 tile on 16x16 MFMAs (T256x352w8m16, mma16w.hip: 4 x 2 waves
+// of 64 x 176, ping-pong schedule), taken before the 32x32 strip for int8
+// inputs whenever the 16x16 tile is allowed (the same pitch rule).
+static const TileCand kRoundStrip16 = {Tile::T256x352w8m16, 256, 352, 1, {0.882658, 0.882658},
+                                       1.3, 0.0, 1.068566, 0.956933};
 
 // Model cost of running an M x N (x batch) product with tile c, in the units
 // of area / eff; `pitch` > 0: the tiles advance `pitch` columns at a time.
@@ -555,6 +616,7 @@ const TileCand &tile_cand(Tile t) {
     if (t == kPitchedRestQ8.t) return kPitchedRestQ8;
     if (t == kRoundWide.t) return kRoundWide;
     if (t == kRoundStrip.t) return kRoundStrip;
+    if (t == kRoundStrip16.t) return kRoundStrip16;
     return kTileCands[0];
 }
 
@@ -690,7 +752,8 @@ MmaPlan plan_mma(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind ki
     const Tile t = pick_tile(M, N, batch, kbytes, kind, in, &cost, m16);
     if (forced) {
         int32_t p = 0;
-        if (batch == 1 && (t == kRoundWide.t || t == kRoundStrip.t)) p = rest_pitch(tile_cand(t), M, N);
+        if (batch == 1 && (t == kRoundWide.t || t == kRoundStrip.t || t == kRoundStrip16.t))
+            p = rest_pitch(tile_cand(t), M, N);
         // (a forced wide tile whose rows do not fit is refused at launch)
         return MmaPlan{t, p, N, t, 0};
     }
@@ -705,8 +768,9 @@ MmaPlan plan_mma(int64_t M, int64_t N, int64_t batch, int64_t kbytes, EpiKind ki
     // the single launch: the layers by 5-25%; the model, whose wide-tile
     // constants are the 256 x 256 eight-wave tile's, cannot rank them).
     if (batch == 1 && in != InType::F32 && wide_round_enabled()) {
-        for (const TileCand *c : {&kRoundStrip, &kRoundWide}) {
+        for (const TileCand *c : {&kRoundStrip16, &kRoundStrip, &kRoundWide}) {
             if (c == &kRoundStrip && in != InType::I8) continue;
+            if (c == &kRoundStrip16 && (in != InType::I8 || !m16_allowed(in, kbytes))) continue;
             if (!wide_fits(*c, ld_b, kbytes)) continue;
             const int32_t p = rest_pitch(*c, M, N);
             if (p <= 256) continue;
@@ -1974,10 +2038,7 @@ gk_workspace *gk_workspace_with_capacity(size_t bytes) {
 
 void gk_workspace_free(gk_workspace *ws) {
     if (!ws) return;
-    if (ws->ptr) {
-        (void)hipDeviceSynchronize();
-        (void)hipFree(ws->ptr);
-    }
+    ws_release(ws);
     delete ws;
 }
 

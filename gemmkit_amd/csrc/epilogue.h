@@ -190,7 +190,11 @@ __device__ __forceinline__ void store4(const EpiParams &ep, int64_t z, int row, 
         }
     }
     if (!ep.vec4 || nvalid < 4) {
-        for (int e = 0; e < nvalid; ++e) {
+        // (a static loop: a runtime bound would index v[] dynamically and
+        // send it through scratch memory)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (e >= nvalid) break;
             if constexpr (K == EpiKind::Q8) {
                 uint8_t *c = (uint8_t *)ep.c + z * ep.bsc + (int64_t)row * ep.rsc +
                              (int64_t)(col + e) * ep.csc;

@@ -101,6 +101,7 @@ enum class Tile : int {
     T256x384w8k128 = 10,  // 2 x 4 waves, 128-byte stages, 2-stage ring; one round at a column pitch
     T256x352w8k128 = 11,  // likewise, 2 x 4 waves over 256 x 256 plus a 96-column strip
     T256x256w8m16 = 12,  // 8 waves, 128-byte stages, 2-stage ring, 16x16 MFMAs (mma16.hip)
+    T256x352w8m16 = 13,  // 8 waves (4 x 2), 16x16 MFMAs, ping-pong, one round at a column pitch (mma16w.hip)
 };
 
 hipError_t launch_mma_i8(Tile tile, const MmaArgs &args, const EpiParams &ep, hipStream_t stream);
@@ -110,6 +111,9 @@ hipError_t launch_mma(InType in, Tile tile, const MmaArgs &args, const EpiParams
 // The 256 x 256 tile on 16x16 matrix-core instructions (mma16.hip): int8
 // (i32, requantized) and bf16 (f32, bf16) output, unsplit, unpitched.
 hipError_t launch_mma16(InType in, const MmaArgs &args, const EpiParams &ep, hipStream_t stream);
+// The 256 x 352 tile on 16x16 matrix-core instructions (mma16w.hip): int8
+// (i32, requantized) output, unsplit, at a column pitch of at most 352.
+hipError_t launch_mma16w(InType in, const MmaArgs &args, const EpiParams &ep, hipStream_t stream);
 
 // Short-contraction route (kstream.hip): K*esz <= kstream_max_kbytes(), the
 // same kernel frame and bit-identical results as launch_mma, 128-row panels

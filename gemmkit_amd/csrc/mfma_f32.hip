@@ -10,6 +10,7 @@ hipError_t launch_mma(InType in, Tile tile, const MmaArgs &args, const EpiParams
     // first row: row strides must be non-negative (the host packs otherwise).
     if (args.lda < 0 || args.ldb < 0) return hipErrorInvalidValue;
     if (tile == Tile::T256x256w8m16) return launch_mma16(in, args, ep, stream);
+    if (tile == Tile::T256x352w8m16) return launch_mma16w(in, args, ep, stream);
     switch (in) {
     case InType::I8: return launch_mma_i8(tile, args, ep, stream);
     case InType::BF16: return launch_mma_bf16(tile, args, ep, stream);

@@ -983,6 +983,7 @@ static hipError_t launch_tile(Tile tile, const MmaArgs &args, const EpiParams &e
     case Tile::T256x384w8k128: return launch_one<T, E, 256, 384, 2, 4, 2, false, 128>(args, ep, stream);
     case Tile::T256x352w8k128: return launch_one<T, E, 256, 352, 2, 4, 2, false, 128>(args, ep, stream);
     case Tile::T256x256w8m16: break;  // mma16.hip (launch_mma dispatches it first)
+    case Tile::T256x352w8m16: break;  // mma16w.hip (likewise)
     }
     return hipErrorInvalidValue;
 }

@@ -44,6 +44,7 @@ class env:
 DEFAULT = {}
 WIDE384 = {"GEMMKIT_HIP_TILE": "256x384w8k128"}
 STRIP352 = {"GEMMKIT_HIP_TILE": "256x352w8k128"}
+STRIP352M16 = {"GEMMKIT_HIP_TILE": "256x352w8m16"}  # int8 only
 SPLIT = {"GEMMKIT_HIP_WIDE": "0"}
 SINGLE = {"GEMMKIT_HIP_WIDE": "0", "GEMMKIT_HIP_TAILSPLIT": "0"}
 
@@ -51,21 +52,21 @@ SINGLE = {"GEMMKIT_HIP_WIDE": "0", "GEMMKIT_HIP_TAILSPLIT": "0"}
 def plans(plan_args, wide=True):
     """The plan under each setting; asserts the tail split is taken with the
     wide plan off, and (wide=True) the one-round plan by default: 256 x 352
-    strip tiles for int8, 256 x 384 tiles for bf16."""
+    tiles on 16x16 MFMAs for int8, 256 x 384 tiles for bf16."""
     with env(**SPLIT):
         assert gk.debug_plan(*plan_args)[1] > 0
     if wide:
         with env(**DEFAULT):
-            want = "256x352w8k128" if plan_args[0] == "i8" else "256x384w8k128"
+            want = "256x352w8m16" if plan_args[0] == "i8" else "256x384w8k128"
             assert gk.debug_plan(*plan_args)[0] == want
 
 
-def both(call):
+def both(call, i8=False):
     """Runs call() under the default plan, the forced 256 x 384 and 256 x 352
-    tiles, the tail split and the single launch; returns (default, 384, 352,
-    split, single)."""
+    tiles (and, i8, the 256 x 352 tile on 16x16 MFMAs), the tail split and the
+    single launch; returns (default, 384, 352[, 352 m16], split, single)."""
     out = []
-    for e in (DEFAULT, WIDE384, STRIP352, SPLIT, SINGLE):
+    for e in (DEFAULT, WIDE384, STRIP352) + ((STRIP352M16,) if i8 else ()) + (SPLIT, SINGLE):
         with env(**e):
             out.append(call())
     return out
@@ -97,7 +98,7 @@ def test_i8_alpha_beta(dev, c_col_major):
         c = c0.clone()
         gk.gemm_i8(3, gk.MatRef.from_row_major(a, m, k), gk.MatRef(b, k, n, 1, k), -2, C(c))
         return c
-    *plans_out, single = both(call)
+    *plans_out, single = both(call, i8=True)
     for o in plans_out:
         assert torch.equal(o, single)
 
@@ -121,7 +122,7 @@ def test_requant(dev, axis, u8):
         fn(gk.MatRef.from_row_major(a, m, k), gk.MatRef(b, k, n, 1, k), req,
            gk.MatMut.from_row_major(c, m, n))
         return c
-    *plans_out, single = both(call)
+    *plans_out, single = both(call, i8=True)
     for o in plans_out:
         assert torch.equal(o, single)
 
@@ -204,6 +205,6 @@ def test_ragged_pitched_rest(dev, kind):
             gk.gemm_i8_requant(gk.MatRef.from_row_major(a, m, k), gk.MatRef(b, k, n, 1, k), req,
                                gk.MatMut.from_row_major(c, m, n))
             return c
-    *plans_out, single = both(call)
+    *plans_out, single = both(call, i8=True)
     for o in plans_out:
         assert torch.equal(o, single)

@@ -65,15 +65,19 @@ def test_m16_tile_exclusions(pick_only, monkeypatch):
     assert gk.debug_plan("bf16", "f32", 4096, 4096, 1024)[0] == "256x256w8m16"
     monkeypatch.setenv("GEMMKIT_HIP_M16", "0")
     assert gk.debug_plan("i8", "i32", 4096, 4096, 4096)[0] != "256x256w8m16"
+    # ... and the one-round layer plan falls back to the 32x32 strip tile
+    monkeypatch.delenv("GEMMKIT_HIP_WIDE", raising=False)
+    monkeypatch.delenv("GEMMKIT_HIP_TAILSPLIT", raising=False)
+    assert gk.debug_plan("i8", "q8", 2048, 11008, 4096)[0] == "256x352w8k128"
 
 
 @pytest.mark.parametrize("shape,pitch,tile", [
-    (("i8", "q8", 2048, 11008, 4096), 344, "256x352w8k128"),
-    (("i8", "i32", 2048, 11008, 4096), 344, "256x352w8k128"),
+    (("i8", "q8", 2048, 11008, 4096), 344, "256x352w8m16"),
+    (("i8", "i32", 2048, 11008, 4096), 344, "256x352w8m16"),
     (("bf16", "bf16", 2048, 11008, 8192), 344, "256x384w8k128"),
     (("bf16", "f32", 2048, 11008, 8192), 344, "256x384w8k128"),
-    (("i8", "i32", 4608, 4608, 4096), 336, "256x352w8k128"),
-    (("i8", "q8", 2000, 11000, 4096), 344, "256x352w8k128"),
+    (("i8", "i32", 4608, 4608, 4096), 336, "256x352w8m16"),
+    (("i8", "q8", 2000, 11000, 4096), 344, "256x352w8m16"),
 ])
 def test_wide_round_of_the_layer_shapes(clean_env, shape, pitch, tile):
     # 8 row tiles of 256 leave 32 tile columns per row for 256 CUs: 11008
@@ -138,6 +142,9 @@ def test_forced_wide_tile_takes_the_round_pitch(clean_env, monkeypatch):
     monkeypatch.setenv("GEMMKIT_HIP_TILE", "256x352w8k128")
     assert gk.debug_plan("i8", "i32", 2048, 11008, 4096, pitches=True) == \
         ("256x352w8k128", 344, 0, "256x352w8k128", 0)
+    monkeypatch.setenv("GEMMKIT_HIP_TILE", "256x352w8m16")
+    assert gk.debug_plan("i8", "i32", 2048, 11008, 4096, pitches=True) == \
+        ("256x352w8m16", 344, 0, "256x352w8m16", 0)
     # no pitch in [192, 384] makes one round: plain 384-wide tiles
     assert gk.debug_plan("i8", "i32", 300, 500, 4096, pitches=True)[1] == 0
 
@@ -170,10 +177,10 @@ def test_wide_tiles_keep_their_rows_within_32bit_offsets(clean_env):
     # 8192 x 2640 int8 products take the one-round strip tile (pitch 336) with
     # packed rows; with B^T rows 8 MB apart its 352 rows would span 2.8 GB of
     # 32-bit buffer offsets, so the plan must not take the wide tiles then.
-    assert gk.debug_plan("i8", "i32", 8192, 2640, 4112, pitches=True)[0] == "256x352w8k128"
+    assert gk.debug_plan("i8", "i32", 8192, 2640, 4112, pitches=True)[0] == "256x352w8m16"
     for ld in (8000016, 6 << 20):
         t = gk.debug_plan("i8", "i32", 8192, 2640, 4112, ld_b=ld)[0]
-        assert t not in ("256x352w8k128", "256x384w8k128"), (ld, t)
+        assert t not in ("256x352w8k128", "256x384w8k128", "256x352w8m16"), (ld, t)
     # the largest stride that still fits keeps it
     ld_max = (0x7FFFFFF0 - 4112) // 351
-    assert gk.debug_plan("i8", "i32", 8192, 2640, 4112, ld_b=ld_max)[0] == "256x352w8k128"
+    assert gk.debug_plan("i8", "i32", 8192, 2640, 4112, ld_b=ld_max)[0] == "256x352w8m16"
