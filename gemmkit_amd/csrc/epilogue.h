@@ -261,4 +261,129 @@ __device__ __forceinline__ void store4(const EpiParams &ep, int64_t z, int row, 
     }
 }
 
+// The requant map on four accumulators of one row (channel scales s, biases
+// b), returned as the four output bytes (element e in byte e).  The same three
+// tiers as store4, fewer instructions in the common one:
+//   * the wave takes requant_bits when some lane's operand reaches 2^24, or
+//     when `tame` is false (the caller has seen a channel scale that is not
+//     finite or reaches 2^100 -- below that, an operand under 2^24 keeps the
+//     f32 product finite, so no per-element overflow check is needed);
+//   * otherwise t = rint of the f32 product, with requant_f32_tie's correction
+//     for the wave when some lane's product sits on a half;
+//   * the zero point and band are applied in f32 with an offset of 128 when
+//     the band reaches below zero (i8 output: the band lies in [-128, 127]),
+//     which puts every in-band value in [0, 255]: one v_med3_f32 clamps it and
+//     one v_cvt_pk_u8_f32 converts and packs it (exact on those integers), and
+//     XOR 0x80 per byte removes the offset, leaving q & 0xFF.  t + zp is exact
+//     wherever the result can land in the band (requant_band).
+__device__ __forceinline__ uint32_t requant_pack4(const EpiParams &ep, const int32_t a[4],
+                                                  const float s[4], const int32_t b[4],
+                                                  bool tame) {
+#pragma clang fp contract(off)
+    float vf[4], ph[4], t[4], d[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        vf[e] = (float)(int32_t)((uint32_t)a[e] + (uint32_t)b[e]);
+        ph[e] = vf[e] * s[e];
+        t[e] = __builtin_rintf(ph[e]);
+        d[e] = ph[e] - t[e];
+    }
+    // |ph - rint(ph)| <= 1/2, so some product sits on a half exactly when the
+    // largest distance is 1/2; likewise one maximum bounds the four operands.
+    const float vmax = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(vf[0]), __builtin_fabsf(vf[1])),
+                                       __builtin_fmaxf(__builtin_fabsf(vf[2]), __builtin_fabsf(vf[3])));
+    const float dmax = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(d[0]), __builtin_fabsf(d[1])),
+                                       __builtin_fmaxf(__builtin_fabsf(d[2]), __builtin_fabsf(d[3])));
+    const bool slow = !tame || !(vmax < 16777216.0f);
+    const bool tie = dmax == 0.5f;
+    if (__builtin_amdgcn_ballot_w64(slow) != 0) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            w |= ((uint32_t)requant_bits(a[e], b[e], __float_as_uint(s[e]), ep.zp, ep.lo, ep.hi) &
+                  0xFFu) << (8 * e);
+        return w;
+    }
+    if (__builtin_amdgcn_ballot_w64(tie) != 0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float pl = __builtin_fmaf(vf[e], s[e], -ph[e]);
+            const bool away = d[e] > 0.0f ? pl > 0.0f : pl < 0.0f;
+            if (__builtin_fabsf(d[e]) == 0.5f && away) t[e] += d[e] + d[e];
+        }
+    }
+    const int32_t off = ep.lo < 0 ? 128 : 0;
+    const float zo = (float)(ep.zp + off), lo = (float)(ep.lo + off), hi = (float)(ep.hi + off);
+    uint32_t w = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        w = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_amdgcn_fmed3f(t[e] + zo, lo, hi), e, w);
+    return off ? w ^ 0x80808080u : w;
+}
+
+// store4 for a chunk wholly inside the matrix with C unit-stride along
+// columns and 4-element aligned (ep.vec4), at the address p of its first
+// element, which the caller steps from chunk to chunk instead of forming it
+// from (row, col) with 64-bit multiplies.  alpha = 1 skips the i32 multiplies;
+// requantized chunks take requant_pack4 (`tame` as there).  Results equal
+// store4's.
+template <EpiKind K, typename A, bool NT = true>
+__device__ __forceinline__ void store4_at(const EpiParams &ep, void *p, const A v[4],
+                                          const float *qs = nullptr, const int32_t *qb = nullptr,
+                                          const float *fb = nullptr, bool tame = true) {
+    if constexpr (K == EpiKind::Q8) {
+        const int32_t a[4] = {(int32_t)v[0], (int32_t)v[1], (int32_t)v[2], (int32_t)v[3]};
+        *(uint32_t *)p = requant_pack4(ep, a, qs, qb, tame);
+    } else if constexpr (K == EpiKind::I32) {
+        typedef int v4i_e __attribute__((ext_vector_type(4)));
+        v4i_e *c = (v4i_e *)p;
+        v4i_e o = {(int32_t)v[0], (int32_t)v[1], (int32_t)v[2], (int32_t)v[3]};
+        if (ep.alpha_i != 1)
+            for (int e = 0; e < 4; ++e) o[e] = (int32_t)((uint32_t)ep.alpha_i * (uint32_t)o[e]);
+        if (ep.beta_i != 0) {
+            v4i_e old = *c;
+            for (int e = 0; e < 4; ++e)
+                o[e] = (int32_t)((ep.beta_i == 1 ? (uint32_t)old[e]
+                                                 : (uint32_t)ep.beta_i * (uint32_t)old[e]) +
+                                 (uint32_t)o[e]);
+        }
+        if constexpr (NT) __builtin_nontemporal_store(o, c);
+        else *c = o;
+    } else if constexpr (K == EpiKind::F32) {
+        typedef float v4f_e __attribute__((ext_vector_type(4)));
+        v4f_e *c = (v4f_e *)p;
+        v4f_e o;
+        for (int e = 0; e < 4; ++e) o[e] = ep.alpha_f * v[e];
+        if (ep.beta_f != 0.0f) {
+            v4f_e old = *c;
+            for (int e = 0; e < 4; ++e)
+                o[e] = ep.beta_f == 1.0f ? old[e] + o[e] : __builtin_fmaf(ep.beta_f, old[e], o[e]);
+        }
+        if (ep.fused) {
+            for (int e = 0; e < 4; ++e) o[e] = fused_apply(ep, o[e], fb[e]);
+        }
+        if constexpr (NT) __builtin_nontemporal_store(o, c);
+        else *c = o;
+    } else {
+        typedef uint32_t v2u_e __attribute__((ext_vector_type(2)));
+        v2u_e *c = (v2u_e *)p;
+        float f[4];
+        for (int e = 0; e < 4; ++e) f[e] = ep.alpha_f * v[e];
+        if (ep.beta_f != 0.0f) {
+            v2u_e old = *c;
+            for (int e = 0; e < 4; ++e) {
+                float w = bf16_widen((uint16_t)(old[e >> 1] >> (16 * (e & 1))));
+                f[e] = ep.beta_f == 1.0f ? w + f[e] : __builtin_fmaf(ep.beta_f, w, f[e]);
+            }
+        }
+        if (ep.fused) {
+            for (int e = 0; e < 4; ++e) f[e] = fused_apply(ep, f[e], fb[e]);
+        }
+        v2u_e o;
+        o[0] = bf16x2_rne(f[0], f[1]);
+        o[1] = bf16x2_rne(f[2], f[3]);
+        __builtin_nontemporal_store(o, c);
+    }
+}
+
 }  // namespace gk

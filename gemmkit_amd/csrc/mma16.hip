@@ -329,6 +329,26 @@ void mma16_kernel(const MmaArgs args, const EpiParams ep) {
         }
     }
     const int gcol0 = n0 + wn * WTN;
+    // A lane's column is fixed and its row advances by RPIT per pass, so its
+    // output address is a per-band base plus a stepped offset (no 64-bit
+    // multiplies per chunk; used by the requantizing store).
+    constexpr int ESZ = E == EpiKind::Q8 ? 1 : (E == EpiKind::BF16 ? 2 : 4);
+    const int64_t row_step = ep.rsc * ESZ;
+    const int64_t out_off = (int64_t)(lane / CPRE) * row_step + (lane % CPRE) * 4 * ESZ;
+    // Whether every channel scale this wave uses is finite and below 2^100
+    // (requant_pack4's fast tier needs no overflow check then).
+    bool tame = true;
+    if constexpr (E == EpiKind::Q8) {
+        static_assert(WTN == 64 && WTM == 128, "one channel per lane (columns) or two (rows)");
+        bool bad;
+        if (ep.axis) {
+            bad = !(__builtin_fabsf(q_scale[wn * WTN + lane]) < 0x1p100f);
+        } else {
+            bad = !(__builtin_fabsf(q_scale[wm * WTM + lane]) < 0x1p100f) ||
+                  !(__builtin_fabsf(q_scale[wm * WTM + 64 + lane]) < 0x1p100f);
+        }
+        tame = __builtin_amdgcn_ballot_w64(bad) == 0;
+    }
     // The requantizing and bf16 stores are long: their row loop stays rolled
     // (unrolled under the unrolled block loop, 32 copies of it thrash the
     // instruction cache: requantized 4096^3 88 against 67 us).
@@ -344,6 +364,8 @@ void mma16_kernel(const MmaArgs args, const EpiParams ep) {
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
         __builtin_amdgcn_wave_barrier();
         const int grow0 = m0 + wm * WTM + i * 16;
+        uint8_t *const cb =
+            (uint8_t *)ep.c + (z * ep.bsc + (int64_t)grow0 * ep.rsc + gcol0) * ESZ + out_off;
 #pragma unroll IT_UNROLL
         for (int it = 0; it < 16 / RPIT; ++it) {
             const int row = it * RPIT + lane / CPRE;
@@ -371,8 +393,18 @@ void mma16_kernel(const MmaArgs args, const EpiParams ep) {
                     for (int e = 0; e < 4; ++e) f4[e] = f;
                 }
             }
-            if (grow < args.M && gcol0 + c4 < n_end)
-                store4<E, val_t, false>(ep, z, grow, gcol0 + c4, n_end, v, s4, b4, f4);
+            if (grow < args.M && gcol0 + c4 < n_end) {
+                // The requantizing store is VALU-bound: whole chunks take the
+                // stepped address and requant_pack4 (requantized 4096^3: 57.8
+                // against 59.7 us).  The i32/f32/bf16 stores are bound by the
+                // write stream; there the per-chunk address costs nothing
+                // measurable and they keep store4.
+                if (E == EpiKind::Q8 && ep.vec4 && gcol0 + c4 + 4 <= n_end)
+                    store4_at<E, val_t, false>(ep, cb + (int64_t)it * RPIT * row_step, v, s4, b4,
+                                               f4, tame);
+                else
+                    store4<E, val_t, false>(ep, z, grow, gcol0 + c4, n_end, v, s4, b4, f4);
+            }
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_wave_barrier();

@@ -256,13 +256,35 @@ void mma16w_kernel(const MmaArgs args, const EpiParams ep) {
 
     // Staged epilogue: each wave's 16 x 176 row bands go to LDS as 16-byte
     // writes and come back as rows, 4 consecutive columns per lane, 44 lanes
-    // per row (11 passes over the 704 chunks of a band).  Per-column channel
-    // scales and biases come as one 16-byte LDS read each per chunk.
+    // per row (11 passes over the 704 chunks of a band).  A lane's row and
+    // chunk advance by 1 row + 20 chunks per pass, so its LDS and output
+    // addresses are stepped, not recomputed: the 64-bit multiplies of a
+    // per-chunk address cost more VALU time than the requantization itself.
+    // Per-column channel scales and biases come as one 16-byte LDS read each
+    // per chunk.
     __syncthreads();
     int32_t *stg = (int32_t *)smem + wave * 16 * EPI_LD;
     typedef int32_t v4_t __attribute__((ext_vector_type(4)));
-    constexpr int CPRE = WTN / 4;  // 44 chunks per staged row
+    typedef float v4f_t __attribute__((ext_vector_type(4)));
+    constexpr int CPRE = WTN / 4;    // 44 chunks per staged row
+    constexpr int STEP = 64 - CPRE;  // chunks a lane moves per pass past one row
+    constexpr int ESZ = E == EpiKind::Q8 ? 1 : 4;
+    static_assert(WTM == 64 && STEP > 0 && STEP < CPRE, "pass stepping assumes 44-chunk rows");
     const int gcol0 = n0 + wn * WTN;
+    // Whether every channel scale this wave uses is finite and below 2^100
+    // (requant_pack4's fast tier needs no overflow check then).
+    bool tame = true;
+    if constexpr (E == EpiKind::Q8) {
+        bool bad = false;
+        if (ep.axis) {
+            for (int c = lane; c < WTN; c += 64)
+                bad = bad || !(__builtin_fabsf(q_scale[wn * WTN + c]) < 0x1p100f);
+        } else {
+            bad = !(__builtin_fabsf(q_scale[wm * WTM + lane]) < 0x1p100f);
+        }
+        tame = __builtin_amdgcn_ballot_w64(bad) == 0;
+    }
+    const int64_t row_step = ep.rsc * ESZ;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -271,19 +293,22 @@ void mma16w_kernel(const MmaArgs args, const EpiParams ep) {
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
         __builtin_amdgcn_wave_barrier();
         const int grow0 = m0 + wm * WTM + i * 16;
+        // element (grow0, gcol0) of C; the lane's chunk is at cb + off
+        uint8_t *const cb =
+            (uint8_t *)ep.c + (z * ep.bsc + (int64_t)grow0 * ep.rsc + gcol0) * ESZ;
+        int row = lane / CPRE, cc = lane % CPRE;
+        int64_t off = row * row_step + 4 * cc * ESZ;
+        int sidx = row * EPI_LD + 4 * cc;  // the chunk's word in the staging rows
 #pragma unroll 1
         for (int it = 0; it < 16 * CPRE / 64; ++it) {
-            const int ci = it * 64 + lane;
-            const int row = ci / CPRE;
-            const int c4 = (ci % CPRE) * 4;
-            const v4_t w = *(const v4_t *)(stg + row * EPI_LD + c4);
+            const int c4 = 4 * cc;
+            const v4_t w = *(const v4_t *)(stg + sidx);
             const int32_t v[4] = {w[0], w[1], w[2], w[3]};
-            const int grow = grow0 + row;
+            const int grow = grow0 + row, gcol = gcol0 + c4;
             float s4[4] = {0, 0, 0, 0};
             int32_t b4[4] = {0, 0, 0, 0};
             if constexpr (E == EpiKind::Q8) {
                 if (ep.axis) {
-                    typedef float v4f_t __attribute__((ext_vector_type(4)));
                     const v4f_t sv = *(const v4f_t *)(q_scale + wn * WTN + c4);
                     const v4_t bv = *(const v4_t *)(q_bias + wn * WTN + c4);
 #pragma unroll
@@ -300,8 +325,22 @@ void mma16w_kernel(const MmaArgs args, const EpiParams ep) {
                     }
                 }
             }
-            if (grow < args.M && gcol0 + c4 < n_end)
-                store4<E, int32_t, false>(ep, z, grow, gcol0 + c4, n_end, v, s4, b4, nullptr);
+            if (grow < args.M && gcol < n_end) {
+                if (ep.vec4 && gcol + 4 <= n_end)
+                    store4_at<E, int32_t, false>(ep, cb + off, v, s4, b4, nullptr, tame);
+                else
+                    store4<E, int32_t, false>(ep, z, grow, gcol, n_end, v, s4, b4, nullptr);
+            }
+            cc += STEP;
+            row += 1;
+            off += row_step + 4 * STEP * ESZ;
+            sidx += EPI_LD + 4 * STEP;
+            if (cc >= CPRE) {
+                cc -= CPRE;
+                row += 1;
+                off += row_step - 4 * CPRE * ESZ;
+                sidx += EPI_LD - 4 * CPRE;
+            }
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_wave_barrier();

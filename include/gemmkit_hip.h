@@ -223,7 +223,15 @@ typedef struct gk_requantize {
     int32_t act;  /* GK_ACT_NONE or GK_ACT_RELU  */
 } gk_requantize;
 
-/* gemm_i8_requant / _with (src/api/int8.rs:230, :280): i8 output, LO/HI = -128/127. */
+/* gemm_i8_requant / _with (src/api/int8.rs:230, :280): i8 output, LO/HI = -128/127.
+ * The per-channel scales are checked (finite, > 0) by copying them to the host,
+ * as the reference checks them when its RequantScale is built.  Under HIP graph
+ * capture nothing can be copied back: a captured call accepts a scale vector
+ * only when an uncaptured call on the same thread has checked one with the same
+ * device pointer and length (the last 64 are remembered), and fails otherwise.
+ * The match is by address: if the caller rewrites that buffer with invalid
+ * scales, or frees it and gets the same address back, a captured call does not
+ * see it (the reference's borrow of the slice makes that impossible there). */
 int gk_gemm_i8_requant(gk_workspace *ws, const gk_mat_ref *a, const gk_mat_ref *b,
                        const gk_requantize *req, const gk_mat_mut *c, gk_par par);
 

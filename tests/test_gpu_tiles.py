@@ -145,3 +145,76 @@ def test_batched_bf16_every_tile(dev, name):
                 assert torch.equal(got.view(torch.int16) if out == torch.bfloat16 else got,
                                    s.view(torch.int16) if out == torch.bfloat16 else s), (name, z)
                 assert (c[z * cbs + m * n:(z + 1) * cbs] == 0).all()
+
+
+EDGE_TILES = [M16, "256x352w8m16", "128x128"]
+
+
+@pytest.mark.parametrize("name", EDGE_TILES)
+@pytest.mark.parametrize("case", ["ties", "big", "nonfinite", "u8relu", "i8relu", "tensor"])
+@pytest.mark.parametrize("axis", [0, 1])
+def test_requant_edges_every_16x16_tile(dev, name, case, axis):
+    """The requantizing store's tiers through the 16x16-MFMA tiles (a 32x32
+    tile as the control), bit-exact against the oracle: products on a half
+    (scale 1/2 on odd accumulators), operands beyond 2^24 (biases near the
+    i32 edges), non-finite and huge channel scales (unchecked entry: inf, NaN,
+    3e38), u8 and i8 output with ReLU, a per-tensor scale.  C's row stride (424) is a
+    multiple of 4 while n = 421 is not, so whole chunks take the vector store
+    and the last chunk of each row the element-wise one."""
+    m, k, n, ldc = 333, 1024, 421, 424
+    a = oracle.rng_i8_sym127(0x721, m * k)
+    b = oracle.rng_i8_sym127(0x722, k * n)
+    ch = n if axis else m
+    u = oracle.rng_unit(0x723 + ch, 2 * ch)
+    scales = (1e-4 + (u[:ch] + 1) / 2 * (1e-2 - 1e-4)).astype(np.float32)
+    bias = np.round(u[ch:] * 65536).astype(np.int32)
+    zp, u8, relu, scale = -3, False, False, 0.0
+    if case == "ties":
+        scales[:] = 0.5
+        bias[::2] += 1
+    elif case == "big":
+        bias[::3] = 2**31 - 1 - np.arange(0, ch, 3, dtype=np.int64) % 1000
+        bias[1::3] = -2**31 + np.arange(1, ch, 3, dtype=np.int64) % 1000
+        scales[::5] = 1e-9
+    elif case == "nonfinite":
+        scales[7] = np.inf
+        scales[100] = np.nan
+        scales[200] = 3e38
+    elif case == "u8relu":
+        zp, u8, relu = 5, True, True
+    elif case == "i8relu":  # the band [3, 127] starts above zero
+        zp, relu = 3, True
+    else:
+        scale, scales = 0.5, None
+    lo, hi = (0, 255) if u8 else (-128, 127)
+    acc = np.zeros(m * n, np.int32)
+    oracle.gemm_i8(m, k, n, 1, a, k, 1, b, 1, k, 0, acc, n, 1)
+    want = np.full(m * ldc, 0x5A, np.uint8)
+    oracle.requant_map(m, n, acc, n, 1, scale, scales, zp, bias, axis,
+                       max(lo, zp) if relu else lo, hi, want, ldc, 1)
+    c = torch.full((m * ldc,), 0x5A, dtype=torch.uint8, device=dev)
+    fn = gk.gemm_i8_requant_u8_unchecked if u8 else gk.gemm_i8_requant_unchecked
+    with tile(name):
+        fn(m, k, n, to_dev(a, dev), k, 1, to_dev(b, dev), 1, k, scale,
+           None if scales is None else to_dev(scales, dev), zp, to_dev(bias, dev), c, ldc, 1,
+           axis=axis, relu=relu)
+    assert np.array_equal(c.cpu().numpy(), want), (name, case, axis)
+
+
+@pytest.mark.parametrize("name", [M16, "256x352w8m16"])
+@pytest.mark.parametrize("alpha,beta", [(1, 0), (1, 1), (-1, 0), (2, -3)])
+def test_i8_stepped_stores_16x16_tiles(dev, name, alpha, beta):
+    """The 16x16-MFMA tiles' stepped-address i32 stores (alpha = 1 without
+    multiplies) with a padded row stride: whole chunks vector-stored, the
+    ragged last chunk element-wise, the padding untouched."""
+    m, k, n, ldc = 517, 640, 389, 392
+    a = oracle.rng_i8_full(0x731, m * k)
+    b = oracle.rng_i8_full(0x732, k * n)
+    c0 = ((np.arange(m * ldc) % 13) - 6).astype(np.int32)
+    want = c0.copy()
+    oracle.gemm_i8(m, k, n, alpha, a, k, 1, b, 1, k, beta, want, ldc, 1)
+    c = to_dev(c0, dev)
+    with tile(name):
+        gk.gemm_i8(alpha, gk.MatRef.from_row_major(to_dev(a, dev), m, k),
+                   gk.MatRef(to_dev(b, dev), k, n, 1, k), beta, gk.MatMut(c, m, n, ldc, 1))
+    assert np.array_equal(c.cpu().numpy(), want)
