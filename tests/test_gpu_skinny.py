@@ -141,6 +141,34 @@ def test_requant_skinny(dev, m, k, n, axis, relu):
     assert np.array_equal(got, want)
 
 
+# Many rows (8192 and up, the decode weights' size): ragged rows, ragged and
+# long K, 3..16 vectors, vectors row-major and strided, alpha/beta.
+WHOLE_ROWS = [(3, 1000, 8200), (8, 4096, 10001), (16, 260, 8193), (5, 4112, 9000),
+              (8, 4096, 14336), (12, 96, 8192)]
+
+
+@pytest.mark.parametrize("m,k,n", WHOLE_ROWS)
+@pytest.mark.parametrize("la", ["row", "col"])
+@pytest.mark.parametrize("alpha,beta", [(1, 0), (3, -2)])
+def test_i8_whole_rows(dev, m, k, n, la, alpha, beta):
+    run_case(dev, m, k, n, alpha, beta, la, "col", "row", seed=13)
+
+
+@pytest.mark.parametrize("axis", [0, 1])
+@pytest.mark.parametrize("relu", [False, True])
+def test_requant_whole_rows(dev, axis, relu):
+    m, k, n = 7, 2064, 9001
+    a = oracle.rng_i8_sym127(510 + m, m * k)
+    b = oracle.rng_i8_sym127(610 + n, k * n)
+    ch = n if axis else m
+    u = oracle.rng_unit(710 + ch, 2 * ch)
+    scales = (1e-4 + (u[:ch] + 1) / 2 * (1e-2 - 1e-4)).astype(np.float32)
+    bias = np.round(u[ch:] * 65536).astype(np.int32)
+    got, want = run_requant(dev, m, k, n, a, b, k, 1, 1, k, 0.0, scales, 3, bias, axis, relu,
+                            False, n, 1, m * n)
+    assert np.array_equal(got, want)
+
+
 def test_batched_skinny_equals_loop(dev):
     """Batched products with a short side of 4: each element bit-equal to a
     standalone call."""
