@@ -14,9 +14,11 @@
 //     for shorter ones), up to S tiles ahead (after the first tile has
 //     landed): a tile's loads take a memory round trip, longer than the
 //     consumers spend on a tile;
-//   * four consumer waves (2 x 2, 64 x 64 each) run the MFMAs of tile t from
-//     LDS, then write tile t through an LDS staging area (one 32 x 32 block at
-//     a time, as whole 128-byte row segments) while later tiles load.
+//   * eight consumer waves (4 x 2, 32 x 64 each) run the MFMAs of tile t
+//     from LDS, then write tile t through a per-wave LDS staging area (16 rows
+//     of a 32 x 32 block at a time, as whole 128-byte row segments) while later
+//     tiles load.  Eight storing waves keep more of the write stream in flight
+//     than four (attention scores 16.0 against 16.9 us in a same-process A/B).
 // The consumer waves issue no loads, so their stores never hold up a wait
 // (loads and stores share one completion counter), and each workgroup writes
 // its tiles back to back instead of all 256 CUs writing at once at the end.
@@ -27,7 +29,7 @@
 namespace gk {
 
 constexpr int kKsTile = 128;                       // tile rows and columns
-constexpr int kKsConsumers = 4;                    // 2 x 2 waves of 64 x 64
+constexpr int kKsConsumers = 8;                    // 4 x 2 waves of 32 x 64
 constexpr int kKsThreads = (kKsConsumers + 1) * 64;
 constexpr int kKsEpiLd = 32 + 4;                   // staging row stride (words)
 
@@ -63,7 +65,7 @@ __global__ __launch_bounds__(kKsThreads) void kstream_kernel(const MmaArgs args,
     constexpr int RPL = 1024 / KB;                  // rows one load fills
     constexpr int CPR = KB / 16;                    // chunks per row
     constexpr int SUB = KB / 32;                    // MFMA sub-steps
-    constexpr int STG = 32 * kKsEpiLd * 4;          // staging bytes per consumer wave
+    constexpr int STG = 16 * kKsEpiLd * 4;          // staging bytes per consumer wave (16 rows)
     constexpr int S = ks_slots<KB>();
     __shared__ __attribute__((aligned(1024))) uint8_t smem[(1 + S) * TILE + kKsConsumers * STG];
     static_assert(sizeof(smem) <= 160 * 1024, "LDS");
@@ -149,9 +151,10 @@ __global__ __launch_bounds__(kKsThreads) void kstream_kernel(const MmaArgs args,
     // ------------------------------------------------------------- consumers
     const int wm = wave >> 1, wn = wave & 1;
     const int lrow = lane & 31, lhalf = lane >> 5;
-    int a_off[2], b_off[2];
+    constexpr int TI = 1;  // 32-row blocks per wave
+    int a_off[TI], b_off[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) a_off[i] = (wm * 64 + i * 32 + lrow) * KB;
+    for (int i = 0; i < TI; ++i) a_off[i] = (wm * 32 * TI + i * 32 + lrow) * KB;
 #pragma unroll
     for (int j = 0; j < 2; ++j) b_off[j] = (wn * 64 + j * 32 + lrow) * KB;
     val_t *const stg = (val_t *)(smem + (1 + S) * TILE + wave * STG);
@@ -162,9 +165,9 @@ __global__ __launch_bounds__(kKsThreads) void kstream_kernel(const MmaArgs args,
     for (int t = 0; t < ntile; ++t) {
         stage_barrier();  // tile t's B landed (and, for t > 0, the previous tile is done)
         const uint8_t *bs = b_lds + (t % S) * TILE;
-        acc_t acc[2][2];
+        acc_t acc[TI][2];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < TI; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j) acc[i][j] = acc_t{};
 #pragma unroll
@@ -172,19 +175,20 @@ __global__ __launch_bounds__(kKsThreads) void kstream_kernel(const MmaArgs args,
             // (block bases are multiples of 32 rows, so the swizzle of row
             // base + lrow is that of lrow)
             const int slot = ks_slot<KB>(lrow, 2 * s + lhalf) << 4;
-            v4i af[2], bf[2];
+            v4i af[TI], bf[2];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) af[i] = *(const v4i *)(a_lds + a_off[i] + slot);
+            for (int i = 0; i < TI; ++i) af[i] = *(const v4i *)(a_lds + a_off[i] + slot);
 #pragma unroll
             for (int j = 0; j < 2; ++j) bf[j] = *(const v4i *)(bs + b_off[j] + slot);
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < TI; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j) acc[i][j] = M::step(bf[j], af[i], acc[i][j]);
         }
-        // Epilogue, one 32 x 32 block at a time through this wave's staging
-        // rows: register 4g+e of lane l is C row l%32, column 8g + 4*(l/32) + e
-        // of the block; rows come back as 128-byte segments (8 lanes a row).
+        // Epilogue, one 32 x 32 block at a time, 16 rows per pass through this
+        // wave's staging rows: register 4g+e of lane l is C row l%32, column
+        // 8g + 4*(l/32) + e of the block; rows come back as 128-byte segments
+        // (8 lanes a row).
         const int n0 = (ch0 + t) * kKsTile;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -201,37 +205,43 @@ __global__ __launch_bounds__(kKsThreads) void kstream_kernel(const MmaArgs args,
                 }
             }
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
+            for (int i = 0; i < TI; ++i) {
                 typedef val_t v4_t __attribute__((ext_vector_type(4)));
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const v4_t w = {(val_t)acc[i][j][4 * g], (val_t)acc[i][j][4 * g + 1],
-                                    (val_t)acc[i][j][4 * g + 2], (val_t)acc[i][j][4 * g + 3]};
-                    *(v4_t *)(stg + lrow * kKsEpiLd + 8 * g + 4 * lhalf) = w;
-                }
-                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): staging writes done
-                __builtin_amdgcn_wave_barrier();
-                const int grow0 = m0 + wm * 64 + i * 32;
+                for (int h = 0; h < 2; ++h) {
+                    // rows 16h .. 16h+15 of the block: lanes holding them stage
+                    if ((lrow >> 4) == h) {
 #pragma unroll
-                for (int it = 0; it < 32 / RPIT; ++it) {
-                    const int row = it * RPIT + lane / CPRE;
-                    const v4_t v4 = *(const v4_t *)(stg + row * kKsEpiLd + c4);
-                    const val_t v[4] = {v4[0], v4[1], v4[2], v4[3]};
-                    const int grow = grow0 + row;
-                    float f4[4] = {col_f[0], col_f[1], col_f[2], col_f[3]};
-                    if constexpr (FB) {
-                        if (ep.fused && !ep.axis) {
-                            const float f =
-                                grow < args.M ? fused_bias<E == EpiKind::BF16>(ep, grow) : 0.0f;
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) f4[e] = f;
+                        for (int g = 0; g < 4; ++g) {
+                            const v4_t w = {(val_t)acc[i][j][4 * g], (val_t)acc[i][j][4 * g + 1],
+                                            (val_t)acc[i][j][4 * g + 2], (val_t)acc[i][j][4 * g + 3]};
+                            *(v4_t *)(stg + (lrow & 15) * kKsEpiLd + 8 * g + 4 * lhalf) = w;
                         }
                     }
-                    if (grow < args.M && gcol0 + c4 < args.N)
-                        store4<E, val_t>(ep, zb, grow, gcol0 + c4, args.N, v, nullptr, nullptr, f4);
+                    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): staging writes done
+                    __builtin_amdgcn_wave_barrier();
+                    const int grow0 = m0 + wm * 32 * TI + i * 32 + 16 * h;
+#pragma unroll
+                    for (int it = 0; it < 16 / RPIT; ++it) {
+                        const int row = it * RPIT + lane / CPRE;
+                        const v4_t v4 = *(const v4_t *)(stg + row * kKsEpiLd + c4);
+                        const val_t v[4] = {v4[0], v4[1], v4[2], v4[3]};
+                        const int grow = grow0 + row;
+                        float f4[4] = {col_f[0], col_f[1], col_f[2], col_f[3]};
+                        if constexpr (FB) {
+                            if (ep.fused && !ep.axis) {
+                                const float f =
+                                    grow < args.M ? fused_bias<E == EpiKind::BF16>(ep, grow) : 0.0f;
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) f4[e] = f;
+                            }
+                        }
+                        if (grow < args.M && gcol0 + c4 < args.N)
+                            store4<E, val_t>(ep, zb, grow, gcol0 + c4, args.N, v, nullptr, nullptr, f4);
+                    }
+                    __builtin_amdgcn_s_waitcnt(0xC07F);  // staging reads done before the next half
+                    __builtin_amdgcn_wave_barrier();
                 }
-                __builtin_amdgcn_s_waitcnt(0xC07F);  // staging reads done before the next block
-                __builtin_amdgcn_wave_barrier();
             }
         }
     }
