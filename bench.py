@@ -615,6 +615,44 @@ def run_extras(args, workloads, want, timed, dev, gk, np, torch, traffic_all, or
         workloads["packed_small_m"] = res
         del bf, pf, bi, pi
 
+    # The vendor library on the same products and operand layouts, timed the
+    # same way (not part of the default run; a comparison, never `value`):
+    # torch._int_mm and torch.mm dispatch to hipBLASLt on this ROCm build.
+    if args.only == "vendor":
+        res = {}
+        M = N = K = 4096
+        ops = 2 * M * N * K
+        a8 = i8(M * K).view(M, K)
+        b8 = i8(N * K).view(N, K).t()  # column-major B via strides
+        c8 = torch.empty(M, N, dtype=torch.int32, device=dev)
+        ms = timed(lambda: torch._int_mm(a8, b8, out=c8), steps, warm)
+        res["i8_gemm_4096"] = {"ms": ms, "TOPS": ops / ms / 1e9, **timed.last}
+        g = torch.Generator().manual_seed(3)
+        ab = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+        bbc = torch.randn(N, K, generator=g).to(torch.bfloat16).to(dev)  # B^T row-major
+        bb = bbc.t()  # column-major B
+        cf = torch.empty(M, N, dtype=torch.float32, device=dev)
+        cb = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        ms = timed(lambda: torch.mm(ab, bb, out=cb), steps, warm)
+        res["bf16_gemm_4096_bf16_out"] = {"ms": ms, "TFLOPS": ops / ms / 1e9, **timed.last}
+        ms = timed(lambda: torch.mm(ab, bb, out_dtype=torch.float32, out=cf), steps, warm) \
+            if "out_dtype" in torch.mm.__doc__ else None
+        if ms is not None:
+            res["bf16_gemm_4096_f32_out"] = {"ms": ms, "TFLOPS": ops / ms / 1e9, **timed.last}
+        # this library on the same bf16 operands, same timing, for the side-by-side
+        ms = timed(lambda: gk.gemm_unchecked(M, K, N, 1.0, ab.view(-1), K, 1, bbc.view(-1), 1, K,
+                                             0.0, cb.view(-1), N, 1),
+                   steps, warm)
+        res["gemmkit_amd_bf16_gemm_4096_bf16_out"] = {"ms": ms, "TFLOPS": ops / ms / 1e9,
+                                                      **timed.last}
+        abf, cff = ab.view(-1), cf.view(-1)
+        ms = timed(lambda: gk.gemm_bf16_f32out(1.0, gk.MatRef(abf, M, K, K, 1),
+                                               gk.MatRef(bbc.view(-1), K, N, 1, K), 0.0,
+                                               gk.MatMut(cff, M, N, N, 1)), steps, warm)
+        res["gemmkit_amd_bf16_gemm_4096_f32_out"] = {"ms": ms, "TFLOPS": ops / ms / 1e9,
+                                                     **timed.last}
+        workloads["vendor"] = res
+
     # a plain elementwise kernel over 1 GiB in, 1 GiB out (reads and writes
     # each byte once): the calibration workload for the HBM byte counters
     if args.only == "copy_1gib":
