@@ -24,6 +24,9 @@
 // its tiles back to back instead of all 256 CUs writing at once at the end.
 // The whole contraction sits in LDS: rows are KB = 64, 128 or 256 bytes
 // (K*esz rounded up to a power of two; bytes past K load as zeros).
+#include <stdlib.h>
+#include <string.h>
+
 #include "mma_kernel.h"
 
 namespace gk {
@@ -276,12 +279,201 @@ static hipError_t ks_go(const MmaArgs &args, const EpiParams &ep, int cus, hipSt
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// kband_kernel -- whole output rows for the widest short contractions: rows of
+// 129..256 bytes of K (KB = 256) and at most 512 columns, with enough
+// 128-row panels (batch elements x row panels) to give every CU one; the
+// attention scores are 256 such panels.
+//
+// Where kstream_kernel writes 128 x 128 tiles (512-byte row pieces), this
+// kernel writes 32-row bands of whole C rows, one store instruction per 1 KiB
+// run of a row, and keeps the write stream free of loads:
+//   * each of the 8 waves owns 64 columns of C and holds those columns' B
+//     rows (all of K) in registers for the workgroup's life (64 VGPRs): it
+//     loads them once, direct-to-LDS into a region of its own (whole 256-byte
+//     rows per 16 lanes, so every load is a full-line read), and reads its
+//     fragments from there (no barrier: no other wave touches the region);
+//     the regions then hold the output staging;
+//   * the workgroup's 128-row A panel goes to LDS by direct-to-LDS loads at
+//     the start, band 0's rows first;
+//   * per 32-row band: each wave's two 32 x 32 blocks (the same instructions,
+//     operand order and k order as the other routes, so every output is
+//     bit-identical), staged in LDS as whole rows, then each wave stores 4
+//     rows as 1 KiB runs (nontemporal).
+// Every load is issued before the first store, so no wait for a load waits
+// on a store (loads and stores share one completion counter): the stores of
+// all four bands go out back to back behind one startup.
+constexpr int kKbBand = 32;          // rows per band
+constexpr int kKbKB = 256;           // K bytes per row (the rest read as zeros)
+
+template <InType T, EpiKind E>
+__global__ __launch_bounds__(512) void kband_kernel(const MmaArgs args, const EpiParams ep,
+                                                    int tiles_m) {
+    using M = Mma<T>;
+    using acc_t = typename M::acc_t;
+    using val_t = typename M::scalar_t;
+    constexpr int esz = (T == InType::I8) ? 1 : (T == InType::BF16 ? 2 : 4);
+    constexpr int NW = 8;                         // waves, 64 columns each
+    constexpr int KB = kKbKB;
+    constexpr int SUB = KB / 32;                  // MFMA sub-steps per 32 x 32 block
+    constexpr int PANEL = 128;                    // rows per workgroup
+    constexpr int NBAND = PANEL / kKbBand;        // 4
+    constexpr int COLS = NW * 64;                 // columns: whole rows of up to 512
+    constexpr int LD = COLS + 4;                  // staging row stride (words)
+    constexpr int CPR = KB / 16;                  // chunks per row
+    constexpr int RPL = 1024 / KB;                // rows one 1 KiB load fills
+    constexpr int A_BYTES = PANEL * KB;
+    constexpr int LPB = kKbBand * KB / 1024 / NW; // A loads per wave per band
+    constexpr int BW_BYTES = 64 * KB;             // one wave's B rows: 16 KiB
+    constexpr int NLB = BW_BYTES / 1024;          // 1 KiB loads of them
+    constexpr int RUNS = COLS / 256;              // store instructions per row (1 KiB for f32 / i32)
+    constexpr int RPW = kKbBand / NW;             // band rows each wave stores
+    static_assert(kKbBand * LD * 4 <= NW * BW_BYTES, "staging fits the B regions");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[A_BYTES + NW * BW_BYTES];
+    static_assert(sizeof(smem) <= 160 * 1024, "LDS");
+    uint8_t *const a_lds = smem;
+    val_t *const stg = (val_t *)(smem + A_BYTES);  // after the B fragments are in registers
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lrow = lane & 31, lhalf = lane >> 5;
+
+    // Unit -> (batch element, row panel), XCD-contiguous: an element's four
+    // panels share its B rows in one XCD's L2.
+    const int64_t unit = xcd_logical(blockIdx.x, gridDim.x);
+    const int64_t zb = unit / tiles_m;
+    const int m0 = (int)(unit % tiles_m) * PANEL;
+
+    const int64_t kbytes = (int64_t)args.K * esz;
+    const int64_t kb16 = (kbytes + 15) / 16 * 16;
+    const int64_t lda_b = args.lda * esz, ldb_b = args.ldb * esz;
+    const uint8_t *A = (const uint8_t *)args.a + zb * args.bsa * esz + (int64_t)m0 * lda_b;
+
+    // A panel: load q = (band*NW + wave)*LPB + u fills LDS bytes
+    // [q*1024, +1024), rows q*RPL + l/CPR, slot l%CPR holding chunk
+    // ks_slot(row, slot); chunks at or past K and rows past M read zeros.
+    const int rows_a = args.M - m0 < PANEL ? args.M - m0 : PANEL;
+    const uint32_t a_num = (uint32_t)((rows_a - 1) * lda_b + kb16);
+    auto load_a = [&](int band) {
+#pragma unroll
+        for (int u = 0; u < LPB; ++u) {
+            const int q = (band * NW + wave) * LPB + u;
+            const int row = q * RPL + lane / CPR;
+            const int c = ks_slot<KB>(row, lane % CPR);
+            const bool in = (int64_t)c * 16 < kbytes && row < rows_a;
+            dma16(A, a_num, in ? (uint32_t)(row * lda_b + c * 16) : kOutOfRange, a_lds + q * 1024);
+        }
+    };
+
+    // This wave's B rows (C columns n0 .. n0+63) into its LDS region, laid
+    // out as the A panel; columns at or past N read zeros (and are not
+    // stored).
+    const int n0 = wave * 64;
+    const int rows_b = args.N - n0 < 64 ? args.N - n0 : 64;
+    const uint8_t *Bw = (const uint8_t *)args.b + zb * args.bsb * esz;
+    const uint32_t b_num = rows_b > 0 ? (uint32_t)((rows_b - 1) * ldb_b + kb16) : 0u;
+    if (rows_b > 0) Bw += (int64_t)n0 * ldb_b;
+    uint8_t *const b_lds = smem + A_BYTES + wave * BW_BYTES;
+
+    load_a(0);
+#pragma unroll
+    for (int q = 0; q < NLB; ++q) {
+        const int row = q * RPL + lane / CPR;
+        const int c = ks_slot<KB>(row, lane % CPR);
+        const bool in = (int64_t)c * 16 < kbytes && row < rows_b;
+        dma16(Bw, b_num, in ? (uint32_t)(row * ldb_b + c * 16) : kOutOfRange, b_lds + q * 1024);
+    }
+#pragma unroll
+    for (int b = 1; b < NBAND; ++b) load_a(b);
+    wait_vmcnt<(NBAND - 1) * LPB>();  // band 0's A rows and this wave's B rows landed
+    // Fragment (s, j) of lane l: row j*32 + l%32, chunk 2s + l/32, as the
+    // other routes' LDS fragment reads lay it out (block bases are multiples
+    // of 32 rows, so the swizzle of row base + lrow is that of lrow).
+    v4i bfr[SUB][2];
+#pragma unroll
+    for (int s = 0; s < SUB; ++s)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            bfr[s][j] = *(const v4i *)(b_lds + (j * 32 + lrow) * KB + (ks_slot<KB>(lrow, 2 * s + lhalf) << 4));
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): B fragments read before the regions hold staging
+    stage_barrier();                     // (and every wave's band 0 A rows landed)
+
+    typedef val_t v4_t __attribute__((ext_vector_type(4)));
+#pragma unroll 1
+    for (int b = 0; b < NBAND; ++b) {
+        acc_t acc[2] = {acc_t{}, acc_t{}};
+        const int arow = b * kKbBand + lrow;
+#pragma unroll
+        for (int s = 0; s < SUB; ++s) {
+            const v4i af = *(const v4i *)(a_lds + arow * KB + (ks_slot<KB>(arow, 2 * s + lhalf) << 4));
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[j] = M::step(bfr[s][j], af, acc[j]);
+        }
+        if (b == 0) wait_vmcnt<0>();  // the other bands' A rows, before any store
+        // Stage: register 4g+e of block j is C row l%32, column
+        // 32j + 8g + 4*(l/32) + e of this wave's 64.
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const v4_t w = {(val_t)acc[j][4 * g], (val_t)acc[j][4 * g + 1],
+                                (val_t)acc[j][4 * g + 2], (val_t)acc[j][4 * g + 3]};
+                *(v4_t *)(stg + lrow * LD + wave * 64 + 32 * j + 8 * g + 4 * lhalf) = w;
+            }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): staging writes done
+        stage_barrier();                     // (and, at band 0, every wave's A rows landed)
+        // Wave w stores band rows RPW*w .. RPW*w + RPW-1, each as RUNS 1 KiB runs.
+        const int64_t grow0 = (int64_t)m0 + b * kKbBand + RPW * wave;
+#pragma unroll
+        for (int i = 0; i < RPW * RUNS; ++i) {
+            const int r = RPW * wave + i / RUNS, col = (i % RUNS) * 256 + 4 * lane;
+            const v4_t v4 = *(const v4_t *)(stg + r * LD + col);
+            const val_t v[4] = {v4[0], v4[1], v4[2], v4[3]};
+            const int64_t grow = grow0 + i / RUNS;
+            if (grow < args.M && col < args.N) store4<E, val_t>(ep, zb, (int)grow, col, args.N, v);
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // staging reads done before the next band's writes
+        stage_barrier();
+    }
+}
+
+// GEMMKIT_HIP_KBAND=0 keeps the widest short contractions on kstream_kernel.
+static bool kband_enabled() {
+    const char *s = getenv("GEMMKIT_HIP_KBAND");
+    return !(s && !strcmp(s, "0"));
+}
+
+// The band kernel takes unfused calls with 129..256 K bytes per row, 257..512
+// columns, rows addressable by 32-bit offsets and at least one 128-row panel
+// per CU (otherwise too few workgroups).  Its arithmetic is the other routes',
+// so which route runs never changes a result.
+template <InType T, EpiKind E>
+static bool kband_takes(const MmaArgs &args, const EpiParams &ep, int cus) {
+    constexpr int esz = (T == InType::I8) ? 1 : (T == InType::BF16 ? 2 : 4);
+    const int64_t kb = (int64_t)args.K * esz;
+    const int64_t kb16 = (kb + 15) / 16 * 16;
+    const int64_t panels = (int64_t)((args.M + 127) / 128) * args.batch;
+    return kband_enabled() && !ep.fused && kb > 128 && kb <= kKbKB && args.N > 256 && args.N <= 512 &&
+           panels >= (cus > 0 ? cus : 256) && panels <= INT32_MAX &&
+           panels_fit(128, 64, args.lda * esz, args.ldb * esz, kb16);
+}
+
+template <InType T, EpiKind E>
+static hipError_t kb_go(const MmaArgs &args, const EpiParams &ep, hipStream_t stream) {
+    const int tiles_m = (args.M + 127) / 128;
+    const int64_t units = (int64_t)tiles_m * args.batch;
+    hipLaunchKernelGGL((kband_kernel<T, E>), dim3((unsigned)units), dim3(512), 0, stream, args, ep,
+                       tiles_m);
+    return hipGetLastError();
+}
+
 template <InType T, EpiKind E>
 static hipError_t ks_kb(const MmaArgs &args, const EpiParams &ep, int cus, hipStream_t stream) {
     constexpr int esz = (T == InType::I8) ? 1 : (T == InType::BF16 ? 2 : 4);
     const int64_t kb = (int64_t)args.K * esz;
     if (kb <= 64) return ks_go<T, E, 64>(args, ep, cus, stream);
     if (kb <= 128) return ks_go<T, E, 128>(args, ep, cus, stream);
+    if (kband_takes<T, E>(args, ep, cus)) return kb_go<T, E>(args, ep, stream);
     return ks_go<T, E, 256>(args, ep, cus, stream);
 }
 
