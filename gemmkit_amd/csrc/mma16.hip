@@ -2,8 +2,9 @@
 // instructions (v_mfma_i32_16x16x64_i8, v_mfma_f32_16x16x32_bf16).
 //
 // Same data path as mma_kernel.h (direct-to-LDS loads of 128-byte stages into
-// a two-stage swizzled ring, fragment reads interleaved with the MFMAs, one
-// barrier per stage, the staged epilogue), with 16x16 blocks: on this chip
+// a swizzled ring -- here three A slots and two B slots, so a stage's A loads
+// go out a stage earlier than its B loads --, fragment reads interleaved with
+// the MFMAs, one barrier per stage, the staged epilogue), with 16x16 blocks: on this chip
 // the 16x16 instructions draw less power per operation than the 32x32 ones,
 // so under the same power limit the clock stays higher (int8 16x16x64:
 // 4.29 POP/s sustained on back-to-back MFMAs at 2.14 GHz, against 3.5 POP/s
@@ -53,22 +54,22 @@ void mma16_kernel(const MmaArgs args, const EpiParams ep) {
     constexpr int NWAVES = 8;
     constexpr int WTM = 128, WTN = 64;
     constexpr int TM = WTM / 16, TN = WTN / 16;  // 8 x 4 blocks of 16 x 16
-    constexpr int STAGE = (BM + BN) * BK;        // 64 KiB
-    constexpr int A_BYTES = BM * BK;
-    constexpr int NI = STAGE / 1024;             // direct-to-LDS instructions per stage
-    constexpr int NIW = NI / NWAVES;             // ... per wave (8)
+    constexpr int ASTAGE = BM * BK, BSTAGE = BN * BK;  // 32 KiB each
+    constexpr int NSA = 3, NSB = 2;              // A and B ring slots
+    constexpr int B_BASE = NSA * ASTAGE;
+    constexpr int LPW = ASTAGE / 1024 / NWAVES;  // loads per wave per operand per stage (4)
     constexpr int RPI = 1024 / BK;               // stage rows one instruction fills
     constexpr int CPR = BK / 16;                 // 16-byte chunks per stage row
     constexpr int EPI_LD = WTN + 4;              // staged-epilogue row stride (words)
-    constexpr int SMEM = 2 * STAGE;
-    static_assert(BM % (NIW * RPI) == 0, "each wave's loads come from one operand");
-    static_assert(NWAVES * 16 * EPI_LD * 4 <= SMEM, "epilogue staging does not fit");
+    constexpr int SMEM = B_BASE + NSB * BSTAGE;  // 160 KiB, all of the CU's LDS
+    constexpr int EPI_BYTES = NWAVES * 16 * EPI_LD * 4;
+    static_assert(SMEM <= 160 * 1024, "LDS");
     using M = Mma16x<T>;
     using acc_t = typename M::acc_t;
     using val_t = typename M::scalar_t;
     constexpr int QCH = (E == EpiKind::Q8) ? BM : 1;
-    constexpr int QBYTES = (E == EpiKind::Q8) ? QCH * 8 : 0;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM + QBYTES];
+    static_assert(EPI_BYTES + QCH * 8 <= SMEM, "epilogue staging and channel table do not fit");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -99,7 +100,6 @@ void mma16_kernel(const MmaArgs args, const EpiParams ep) {
     const uint8_t *A = (const uint8_t *)args.a + zb * args.bsa * esz;
     const uint8_t *B = (const uint8_t *)args.b + zb * args.bsb * esz;
     const int KT = (int)((kbytes + BK - 1) / BK);
-    const bool k_whole = (kbytes % BK) == 0;
 
     // Operand panels as buffer resources (rows past the matrix edge read
     // zeros), as in mma_kernel.
@@ -109,43 +109,38 @@ void mma16_kernel(const MmaArgs args, const EpiParams ep) {
     const uint32_t a_num = (uint32_t)(((args.M - m0 < BM ? args.M - m0 : BM) - 1) * lda_b + kb16);
     const uint32_t b_num = (uint32_t)(((args.N - n0 < BN ? args.N - n0 : BN) - 1) * ldb_b + kb16);
 
-    // Loads: wave w fills stage bytes [w*NIW*1024, (w+1)*NIW*1024), all from
-    // one operand; instruction i's rows lie RPI*i below instruction 0's and
-    // its chunk repeats every two instructions (the swizzle).
-    uint32_t voff[2];
+    // Loads: wave w fills rows [w*LPW*RPI, +LPW*RPI) of an A stage and of a B
+    // stage; instruction i's rows lie RPI*i below instruction 0's and its
+    // chunk repeats every two instructions (the swizzle).
+    uint32_t voa[2], vob[2];
     int kch[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const int q = wave * NIW + i;
-        const int row = q * RPI + lane / CPR;
+        const int row = (wave * LPW + i) * RPI + lane / CPR;
         const int ch = (lane % CPR) ^ swz_of<BK>(row);
         kch[i] = ch * 16;
-        voff[i] = q * RPI < BM ? (uint32_t)(row * lda_b + ch * 16)
-                               : (uint32_t)((row - BM) * ldb_b + ch * 16);
+        voa[i] = (uint32_t)(row * lda_b + ch * 16);
+        vob[i] = (uint32_t)(row * ldb_b + ch * 16);
     }
-    const bool w_from_a = wave * NIW * RPI < BM;
-    const uint8_t *const w_pan = w_from_a ? a_pan : b_pan;
-    const uint32_t w_num = w_from_a ? a_num : b_num;
-    const uint32_t rstep = (uint32_t)(RPI * (w_from_a ? lda_b : ldb_b));
-    auto lane_off = [&](int i) -> uint32_t { return voff[i % 2] + (uint32_t)(i - i % 2) * rstep; };
-    auto issue_stage = [&](int kt, int slot, int first, int count) {
-        const uint32_t kb = (uint32_t)kt * BK;
-        uint8_t *dst = smem + slot * STAGE + wave * NIW * 1024;
-        const bool dead = kt >= KT;
-        const bool tail = !k_whole && kt == KT - 1;
-#pragma unroll
-        for (int i = first; i < first + count; ++i) {
-            uint32_t off = lane_off(i) + kb;
-            if (dead || (tail && (int64_t)kb + kch[i % 2] >= kbytes)) off = kOutOfRange;
-            dma16(w_pan, w_num, off, dst + i * 1024);
-        }
-    };
+    const uint32_t rsa = (uint32_t)(RPI * lda_b), rsb = (uint32_t)(RPI * ldb_b);
     const bool soff_ok = lda_b >= kb16 && ldb_b >= kb16;
-    auto issue_whole = [&](int kt, int slot, int first, int count) {
+    // Load i of operand X (0: A, 1: B) of stage kt into its slot; stages wholly
+    // inside K take the stage offset in the scalar operand.
+    auto load1 = [&](auto whole, int X, int kt, int slot, int i) {
         const uint32_t kb = (uint32_t)kt * BK;
-        uint8_t *dst = smem + slot * STAGE + wave * NIW * 1024;
-#pragma unroll
-        for (int i = first; i < first + count; ++i) dma16s(w_pan, w_num, lane_off(i), kb, dst + i * 1024);
+        const uint32_t lo = X == 0 ? voa[i % 2] + (uint32_t)(i - i % 2) * rsa
+                                   : vob[i % 2] + (uint32_t)(i - i % 2) * rsb;
+        const uint8_t *pan = X == 0 ? a_pan : b_pan;
+        const uint32_t num = X == 0 ? a_num : b_num;
+        uint8_t *dst = smem + (X == 0 ? slot * ASTAGE : B_BASE + slot * BSTAGE) +
+                       (wave * LPW + i) * 1024;
+        if constexpr (decltype(whole)::value) {
+            dma16s(pan, num, lo, kb, dst);
+        } else {
+            uint32_t off = lo + kb;
+            if (kt >= KT || (int64_t)kb + kch[i % 2] >= kbytes) off = kOutOfRange;
+            dma16(pan, num, off, dst);
+        }
     };
 
     acc_t acc[TM][TN];
@@ -156,7 +151,7 @@ void mma16_kernel(const MmaArgs args, const EpiParams ep) {
 
     const int l16 = lane & 15, lq = lane >> 4;
     const int a_off0 = (wm * WTM + l16) * BK;             // + i*16*BK for block i
-    const int b_off0 = A_BYTES + (wn * WTN + l16) * BK;   // + j*16*BK for block j
+    const int b_off0 = (wn * WTN + l16) * BK;             // + j*16*BK for block j
     const int swz = swz_of<BK>(l16);  // block bases are multiples of 16 rows
     auto slot_of = [&](int ss) { return ((4 * ss + lq) ^ swz) << 4; };
 
@@ -168,18 +163,16 @@ void mma16_kernel(const MmaArgs args, const EpiParams ep) {
             for (int j = 0; j < TN; ++j) acc[i][j] = M::step(bf[set][j], af[set][i], acc[i][j]);
     };
     // Program-order memory operations of a phase: A reads of blocks
-    // [alo, alo+NA) and (WB) the B reads, with NL loads of stage st into
-    // `slot` spread among them (op_is_load); whole stages take scalar-offset
-    // loads.
-    auto ops = [&](auto whole, const uint8_t *src, int ss, int set, int alo, auto na, auto wb,
-                   auto nl, int st, int slot, int first) {
-        constexpr bool WHOLE = decltype(whole)::value;
+    // [alo, alo+NA) from stage sa and (WB) the B reads from stage sb, with NL
+    // loads (ld(l), l = 0..NL-1) spread among them (op_is_load).
+    auto ops = [&](const uint8_t *sa, const uint8_t *sb, int ss, int set, int alo, auto na, auto wb,
+                   auto nl, auto ld) {
         constexpr int NA = decltype(na)::value;
         constexpr int NB = decltype(wb)::value ? TN : 0;
         constexpr int NR = NA + NB;
         constexpr int NL = decltype(nl)::value;
         const int sl = slot_of(ss);
-        int l = first;
+        int l = 0;
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
             // Order: A[alo], the B fragments, then A[alo+1 ..]: the next
@@ -189,23 +182,21 @@ void mma16_kernel(const MmaArgs args, const EpiParams ep) {
             const int ra = r == 0 ? 0 : (r <= NB ? -1 : r - NB);
             const int rbi = r - (NA > 0 ? 1 : 0);
             if (NA > 0 && ra >= 0)
-                af[set][alo + ra] = *(const v4i *)(src + a_off0 + (alo + ra) * 16 * BK + sl);
+                af[set][alo + ra] = *(const v4i *)(sa + a_off0 + (alo + ra) * 16 * BK + sl);
             else
-                bf[set][rbi] = *(const v4i *)(src + b_off0 + rbi * 16 * BK + sl);
+                bf[set][rbi] = *(const v4i *)(sb + b_off0 + rbi * 16 * BK + sl);
             if ((r + 1) * NL / NR != r * NL / NR) {
-                if constexpr (WHOLE)
-                    issue_whole(st, slot, l, 1);
-                else
-                    issue_stage(st, slot, l, 1);
+                ld(l);
                 ++l;
             }
         }
     };
 
-    // Requantization channels staged in LDS (see mma_kernel).
+    // Requantization channels: loaded now, staged in LDS beside the epilogue
+    // staging once the ring is free (see mma_kernel).
     constexpr int QPT = (QCH + NWAVES * 64 - 1) / (NWAVES * 64);
-    float *const q_scale = (float *)(smem + SMEM);
-    int32_t *const q_bias = (int32_t *)(smem + SMEM + QCH * 4);
+    float *const q_scale = (float *)(smem + EPI_BYTES);
+    int32_t *const q_bias = (int32_t *)(smem + EPI_BYTES + QCH * 4);
     int q_ch0 = 0, q_n = 0;
     float q_s[QPT] = {};
     int32_t q_b[QPT] = {};
@@ -223,18 +214,95 @@ void mma16_kernel(const MmaArgs args, const EpiParams ep) {
         }
     }
 
-    // Load schedule: stage kt+2's loads go into stage kt's slot as soon as the
-    // barrier that ends the reads of stage kt allows, all of them under stage
-    // kt's last phase (P0), so each has three phases to land.  (At this
-    // kernel's higher clock the 32x32 tile's split -- a third there, the rest
-    // under stage kt+1's first two phases -- leaves the last loads too little
-    // time: 63.5-65.6 against 59.4-61.5 us on int8 4096^3.  Giving the A
-    // panel a third 32 KiB slot instead, its loads two stages ahead, measured
-    // 63.2-63.8 us.)
-    constexpr int P0 = NIW, P1 = 0, P2 = 0;
-    issue_stage(0, 0, 0, NIW);
-    issue_stage(1, 1, 0, P0);
-    wait_vmcnt<P0>();
+    // Load schedule: stage kt+2's A loads go out under stage kt's first phase
+    // (A slot (kt+2)%3 last held stage kt-1, whose reads ended before stage
+    // kt-1's barrier), its B loads under stage kt's last phase, after the
+    // barrier that ends stage kt's B reads; both are waited for at stage
+    // kt+1's barrier, with the four A loads per wave of stage kt+3 still in
+    // flight.  The A loads thus have two stages to land and the B loads,
+    // issued before them in the address unit's queue, one: with all of a
+    // stage's loads after the barrier in a two-slot ring they landed late
+    // (int8 4096^3 main loop 78.5k against 73.9k shader cycles per
+    // workgroup; bf16 157.8k against 146.0k).
+    using ZL = std::integral_constant<int, 0>;
+    using LW = std::integral_constant<int, LPW>;
+    auto noload = [](int) {};
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) load1(std::false_type{}, 0, 0, 0, i);
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) load1(std::false_type{}, 1, 0, 0, i);
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) load1(std::false_type{}, 0, 1, 1, i);
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) load1(std::false_type{}, 1, 1, 1, i);
+    wait_vmcnt<2 * LPW>();  // stage 0 landed
+    stage_barrier();
+    {
+        using NA = std::integral_constant<int, TM>;
+        ops(smem, smem + B_BASE, 0, 0, 0, NA{}, std::true_type{}, ZL{}, noload);
+    }
+
+    constexpr int NM = (TM / 2) * TN;  // MFMAs per phase (16)
+    constexpr int SPAN = NM * 7 / 8;
+    const int ktw = (int)(kbytes / BK);
+    // sa: stage kt's A slot (kt % 3).
+    auto kstep = [&](int kt, int sa, auto whole) {
+        using H = std::integral_constant<int, TM / 2>;
+        using FA = std::integral_constant<int, TM>;
+        const int sa1 = sa == NSA - 1 ? 0 : sa + 1, sa2 = sa1 == NSA - 1 ? 0 : sa1 + 1;
+        const uint8_t *s_a = smem + sa * ASTAGE, *s_b = smem + B_BASE + (kt & 1) * BSTAGE;
+        const uint8_t *n_a = smem + sa1 * ASTAGE, *n_b = smem + B_BASE + ((kt + 1) & 1) * BSTAGE;
+        auto ld_a = [&](int i) { load1(whole, 0, kt + 2, sa2, i); };
+        auto ld_b = [&](int i) { load1(whole, 1, kt + 2, kt & 1, i); };
+        // phase 0: sub-step 0, blocks 0-3; read sub-step 1's A 0-3 and B;
+        // stage kt+2's A loads
+        mfma_rows(0, 0);
+        ops(s_a, s_b, 1, 1, 0, H{}, std::true_type{}, LW{}, ld_a);
+        sched_ops<NM, TM / 2 + TN, LPW, SPAN>();
+        // phase 1: sub-step 0, blocks 4-7; read sub-step 1's A 4-7
+        mfma_rows(0, TM / 2);
+        ops(s_a, s_b, 1, 1, TM / 2, H{}, std::false_type{}, ZL{}, noload);
+        sched_ops<NM, TM / 2, 0, SPAN>();
+        // phase 2: sub-step 1, blocks 0-3; stage kt+1 landed (the A loads of
+        // stage kt+2 may fly), then the barrier
+        mfma_rows(1, 0);
+#pragma unroll
+        for (int m = 0; m < NM; ++m) __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[0][i]));
+#pragma unroll
+        for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bf[0][j]));
+        wait_vmcnt<LPW>();
+        stage_barrier();
+#pragma unroll
+        for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[1][i]));
+#pragma unroll
+        for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bf[1][j]));
+        // phase 3: sub-step 1, blocks 4-7; read stage kt+1's sub-step 0;
+        // stage kt+2's B loads
+        mfma_rows(1, TM / 2);
+        ops(n_a, n_b, 0, 0, 0, FA{}, std::true_type{}, LW{}, ld_b);
+        sched_ops<NM, TM + TN, LPW, SPAN>();
+    };
+    // Stages whose loads (of stage kt+2) lie wholly inside K take the
+    // scalar-offset loads.
+    const int kt_whole = soff_ok ? (ktw - 2 > 0 ? ktw - 2 : 0) : 0;
+    int kt = 0, sa = 0;
+    for (; kt < kt_whole; ++kt) {
+        kstep(kt, sa, std::true_type{});
+        sa = sa == NSA - 1 ? 0 : sa + 1;
+    }
+    for (; kt < KT; ++kt) {
+        kstep(kt, sa, std::false_type{});
+        sa = sa == NSA - 1 ? 0 : sa + 1;
+    }
+
+    // Staged epilogue, 16 rows per block: each 16 x 64 row band of the wave
+    // goes to LDS as 16-byte writes (EPI_LD = 4 mod 64 words: conflict-free)
+    // and comes back as rows, 16 lanes per row, whole 16-byte chunks.  The
+    // loads issued past the end of K (zeros into ring slots) land first.
+    wait_vmcnt<0>();
+    __syncthreads();
     if constexpr (E == EpiKind::Q8) {
 #pragma unroll
         for (int u = 0; u < QPT; ++u) {
@@ -244,65 +312,8 @@ void mma16_kernel(const MmaArgs args, const EpiParams ep) {
                 q_bias[c] = q_b[u];
             }
         }
+        __syncthreads();
     }
-    stage_barrier();
-    {
-        using Z = std::integral_constant<int, 0>;
-        using NA = std::integral_constant<int, TM>;
-        ops(std::false_type{}, smem, 0, 0, 0, NA{}, std::true_type{}, Z{}, 0, 0, 0);
-    }
-
-    constexpr int NM = (TM / 2) * TN;  // MFMAs per phase (16)
-    constexpr int SPAN = NM * 7 / 8;
-    const int ktw = (int)(kbytes / BK);
-    auto kstep = [&](int kt, auto whole) {
-        using L0 = std::integral_constant<int, P0>;
-        using L1 = std::integral_constant<int, P1>;
-        using L2 = std::integral_constant<int, P2>;
-        using LN = std::integral_constant<int, 0>;
-        using H = std::integral_constant<int, TM / 2>;
-        using FA = std::integral_constant<int, TM>;
-        using A0 = std::integral_constant<int, 0>;
-        const uint8_t *s = smem + (kt & 1) * STAGE;
-        const int nslot = (kt + 1) & 1;
-        // phase 0: sub-step 0, blocks 0-3; read sub-step 1's A 0-3 and B
-        mfma_rows(0, 0);
-        ops(whole, s, 1, 1, 0, H{}, std::true_type{}, L1{}, kt + 1, nslot, P0);
-        sched_ops<NM, TM / 2 + TN, P1, SPAN>();
-        // phase 1: sub-step 0, blocks 4-7; read sub-step 1's A 4-7
-        mfma_rows(0, TM / 2);
-        ops(whole, s, 1, 1, TM / 2, H{}, std::false_type{}, L2{}, kt + 1, nslot, P0 + P1);
-        sched_ops<NM, TM / 2, P2, SPAN>();
-        // phase 2: sub-step 1, blocks 0-3
-        mfma_rows(1, 0);
-#pragma unroll
-        for (int m = 0; m < NM; ++m) __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-#pragma unroll
-        for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[0][i]));
-#pragma unroll
-        for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bf[0][j]));
-        wait_vmcnt<0>();
-        stage_barrier();
-#pragma unroll
-        for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[1][i]));
-#pragma unroll
-        for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bf[1][j]));
-        // phase 3: sub-step 1, blocks 4-7; read stage kt+1's sub-step 0
-        mfma_rows(1, TM / 2);
-        ops(whole, smem + nslot * STAGE, 0, 0, 0, FA{}, std::true_type{}, L0{}, kt + 2, kt & 1, 0);
-        sched_ops<NM, TM + TN, P0, SPAN>();
-        (void)LN{};
-        (void)A0{};
-    };
-    const int kt_whole = soff_ok ? (ktw - 2 < KT ? (ktw - 2 > 0 ? ktw - 2 : 0) : KT) : 0;
-    int kt = 0;
-    for (; kt < kt_whole; ++kt) kstep(kt, std::true_type{});
-    for (; kt < KT; ++kt) kstep(kt, std::false_type{});
-
-    // Staged epilogue, 16 rows per block: each 16 x 64 row band of the wave
-    // goes to LDS as 16-byte writes (EPI_LD = 4 mod 64 words: conflict-free)
-    // and comes back as rows, 16 lanes per row, whole 16-byte chunks.
-    __syncthreads();
     val_t *stg = (val_t *)smem + wave * 16 * EPI_LD;
     typedef val_t v4_t __attribute__((ext_vector_type(4)));
     constexpr bool FB = E == EpiKind::F32 || E == EpiKind::BF16;
