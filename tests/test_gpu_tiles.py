@@ -151,12 +151,12 @@ EDGE_TILES = [M16, "256x352w8m16", "128x128"]
 
 
 @pytest.mark.parametrize("name", EDGE_TILES)
-@pytest.mark.parametrize("case", ["ties", "big", "nonfinite", "u8relu", "i8relu", "tensor"])
+@pytest.mark.parametrize("case", ["ties", "onehalf", "big", "nonfinite", "u8relu", "i8relu", "tensor"])
 @pytest.mark.parametrize("axis", [0, 1])
 def test_requant_edges_every_16x16_tile(dev, name, case, axis):
     """The requantizing store's tiers through the 16x16-MFMA tiles (a 32x32
     tile as the control), bit-exact against the oracle: products on a half
-    (scale 1/2 on odd accumulators), operands beyond 2^24 (biases near the
+    (scale 1/2 on odd accumulators, for every channel or for one), operands beyond 2^24 (biases near the
     i32 edges), non-finite and huge channel scales (unchecked entry: inf, NaN,
     3e38), u8 and i8 output with ReLU, a per-tensor scale.  C's row stride (424) is a
     multiple of 4 while n = 421 is not, so whole chunks take the vector store
@@ -172,6 +172,8 @@ def test_requant_edges_every_16x16_tile(dev, name, case, axis):
     if case == "ties":
         scales[:] = 0.5
         bias[::2] += 1
+    elif case == "onehalf":  # one channel on halves: single chunks of a row block need the tie tier
+        scales[37] = 0.5
     elif case == "big":
         bias[::3] = 2**31 - 1 - np.arange(0, ch, 3, dtype=np.int64) % 1000
         bias[1::3] = -2**31 + np.arange(1, ch, 3, dtype=np.int64) % 1000
