@@ -329,9 +329,15 @@ def main():
         with open(upath) as f:
             u = json.load(f).get("i8_gemm_4096")
         if u:
-            mfma_util = {"value": u["mfma_util"], "clock_ghz": u["clock_ghz"],
+            # GRBM_GUI_ACTIVE does not tick at the shader clock (a shader-clock
+            # counter, s_memtime against the 100 MHz s_memrealtime, puts the
+            # shader clock of this kernel at about 1.75 GHz where the GRBM
+            # figure reads above 2.1), so the rate it gives is reported under
+            # its own name.
+            mfma_util = {"value": u["mfma_util"], "grbm_gui_active_ghz": u["clock_ghz"],
                          "source": "rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD "
-                                   "x 1024 SIMDs), eager launches; profiles/mfma_util.json"}
+                                   "x 1024 SIMDs) (rocprof's MfmaUtil), eager launches; "
+                                   "profiles/mfma_util.json"}
     line = {
         "metric": "int8 GEMM TOPS + MFMA util at 4096³; bf16 TFLOPS; GEMV HBM GB/s",
         "value": value,
