@@ -147,6 +147,48 @@ struct Store<EpiKind::Q8> {
 };
 
 
+// Cache policy of an output store.
+//   Plain  write-back: the line stays dirty in the XCD's L2 and reaches the
+//          256 MB Infinity Cache when evicted or at the kernel's end;
+//   NT     nontemporal (streamed towards HBM): outputs written once while other
+//          data streams, such as the short-contraction kernel's rotating batches
+//          (the big tiles measured 1.7 us slower with it on 4096^3 i32 and 2 us on
+//          bf16 4096^3 with f32 out; the batched attention scores 4 us faster);
+//   WT     write-back with the sc1 (device scope) bit, which writes the line
+//          through the L2 as it is stored.  Same-process A/Bs on three boxes:
+//          the requantizing layer 2048x4096x11008 78.7 / 79.7 / 79.6 against
+//          80.7 / 81.8 / 81.7 us; int8 4096^3 with i32 out 56.2 / 58.8 / 58.3
+//          against 57.7 / 58.4 / 58.1 (box-dependent, kept for the same
+//          write pattern); f32 and bf16 outputs measured no change and keep
+//          Plain / NT;
+//   NTWT   nontemporal with sc1: the band kernel's attention scores
+//          15.2-15.4 against 15.5-15.7 us with NT alone (four A/Bs).
+// Every policy stores the same bytes; only where the line is kept differs.
+enum class StPol { Plain, NT, WT, NTWT };
+
+// The requantized words follow WT and are stored Plain otherwise.
+constexpr StPol q8_pol(StPol p) { return p == StPol::WT ? StPol::WT : StPol::Plain; }
+
+template <StPol P, typename V>
+__device__ __forceinline__ void st_out(V *p, V v) {
+    static_assert(sizeof(V) == 16 || sizeof(V) == 4, "16-byte chunks or 4-byte words");
+    if constexpr (P == StPol::Plain) {
+        *p = v;
+    } else if constexpr (P == StPol::NT) {
+        __builtin_nontemporal_store(v, p);
+    } else if constexpr (sizeof(V) == 16) {
+        if constexpr (P == StPol::WT)
+            asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+        else
+            asm volatile("global_store_dwordx4 %0, %1, off nt sc1" : : "v"(p), "v"(v) : "memory");
+    } else {
+        if constexpr (P == StPol::WT)
+            asm volatile("global_store_dword %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+        else
+            asm volatile("global_store_dword %0, %1, off nt sc1" : : "v"(p), "v"(v) : "memory");
+    }
+}
+
 // Four consecutive output columns (col .. col+3) of one row, from the
 // LDS-staged accumulators.  `vec` (uniform) says C is unit-stride along columns
 // and 4-element aligned, so whole chunks take one vector access; otherwise, and
@@ -156,13 +198,9 @@ struct Store<EpiKind::Q8> {
 // wave when any lane's product sits on a half, and the exact integer path for
 // every lane of the wave when any lane needs it.
 // For F32/BF16 with a fused epilogue, fb holds the four elements' bias values.
-// NT selects nontemporal stores for the i32 and f32 chunks: right for outputs
-// written once while other data streams (the short-contraction kernel's
-// rotating batches); the big-tile kernel stores i32/f32 normally, leaving its
-// output in the 256 MB Infinity Cache for whatever reads it next (1.7 us
-// faster on 4096^3 i32, 2 us on bf16 4096^3 with f32 out; 4 us slower on the
-// batched attention scores, which stay nontemporal).
-template <EpiKind K, typename A, bool NT = true>
+// P is the cache policy of the i32, f32 and requantized stores (StPol); bf16
+// chunks are always stored nontemporally.
+template <EpiKind K, typename A, StPol P = StPol::NT>
 __device__ __forceinline__ void store4(const EpiParams &ep, int64_t z, int row, int col, int ncols,
                                        const A v[4], const float *qs = nullptr,
                                        const int32_t *qb = nullptr, const float *fb = nullptr) {
@@ -218,8 +256,7 @@ __device__ __forceinline__ void store4(const EpiParams &ep, int64_t z, int row, 
                                                  : (uint32_t)ep.beta_i * (uint32_t)old[e]) +
                                  (uint32_t)o[e]);
         }
-        if constexpr (NT) __builtin_nontemporal_store(o, c);
-        else *c = o;
+        st_out<P>(c, o);
     } else if constexpr (K == EpiKind::F32) {
         typedef float v4f_e __attribute__((ext_vector_type(4)));
         v4f_e *c = (v4f_e *)((float *)ep.c + off);
@@ -233,8 +270,7 @@ __device__ __forceinline__ void store4(const EpiParams &ep, int64_t z, int row, 
         if (ep.fused) {
             for (int e = 0; e < 4; ++e) o[e] = fused_apply(ep, o[e], fb[e]);
         }
-        if constexpr (NT) __builtin_nontemporal_store(o, c);
-        else *c = o;
+        st_out<P>(c, o);
     } else if constexpr (K == EpiKind::BF16) {
         typedef uint32_t v2u_e __attribute__((ext_vector_type(2)));
         v2u_e *c = (v2u_e *)((uint16_t *)ep.c + off);
@@ -257,7 +293,7 @@ __device__ __forceinline__ void store4(const EpiParams &ep, int64_t z, int row, 
     } else {
         const uint32_t word = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
                               ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)q[3] << 24);
-        *(uint32_t *)((uint8_t *)ep.c + off) = word;
+        st_out<q8_pol(P)>((uint32_t *)((uint8_t *)ep.c + off), word);
     }
 }
 
@@ -327,13 +363,13 @@ __device__ __forceinline__ uint32_t requant_pack4(const EpiParams &ep, const int
 // from (row, col) with 64-bit multiplies.  alpha = 1 skips the i32 multiplies;
 // requantized chunks take requant_pack4 (`tame` as there).  Results equal
 // store4's.
-template <EpiKind K, typename A, bool NT = true>
+template <EpiKind K, typename A, StPol P = StPol::NT>
 __device__ __forceinline__ void store4_at(const EpiParams &ep, void *p, const A v[4],
                                           const float *qs = nullptr, const int32_t *qb = nullptr,
                                           const float *fb = nullptr, bool tame = true) {
     if constexpr (K == EpiKind::Q8) {
         const int32_t a[4] = {(int32_t)v[0], (int32_t)v[1], (int32_t)v[2], (int32_t)v[3]};
-        *(uint32_t *)p = requant_pack4(ep, a, qs, qb, tame);
+        st_out<q8_pol(P)>((uint32_t *)p, requant_pack4(ep, a, qs, qb, tame));
     } else if constexpr (K == EpiKind::I32) {
         typedef int v4i_e __attribute__((ext_vector_type(4)));
         v4i_e *c = (v4i_e *)p;
@@ -347,8 +383,7 @@ __device__ __forceinline__ void store4_at(const EpiParams &ep, void *p, const A 
                                                  : (uint32_t)ep.beta_i * (uint32_t)old[e]) +
                                  (uint32_t)o[e]);
         }
-        if constexpr (NT) __builtin_nontemporal_store(o, c);
-        else *c = o;
+        st_out<P>(c, o);
     } else if constexpr (K == EpiKind::F32) {
         typedef float v4f_e __attribute__((ext_vector_type(4)));
         v4f_e *c = (v4f_e *)p;
@@ -362,8 +397,7 @@ __device__ __forceinline__ void store4_at(const EpiParams &ep, void *p, const A 
         if (ep.fused) {
             for (int e = 0; e < 4; ++e) o[e] = fused_apply(ep, o[e], fb[e]);
         }
-        if constexpr (NT) __builtin_nontemporal_store(o, c);
-        else *c = o;
+        st_out<P>(c, o);
     } else {
         typedef uint32_t v2u_e __attribute__((ext_vector_type(2)));
         v2u_e *c = (v2u_e *)p;

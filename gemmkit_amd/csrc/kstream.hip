@@ -299,7 +299,7 @@ static hipError_t ks_go(const MmaArgs &args, const EpiParams &ep, int cus, hipSt
 //   * per 32-row band: each wave's two 32 x 32 blocks (the same instructions,
 //     operand order and k order as the other routes, so every output is
 //     bit-identical), staged in LDS as whole rows, then each wave stores 4
-//     rows as 1 KiB runs (nontemporal).
+//     rows as 1 KiB runs (nontemporal, written through the L2: StPol::NTWT).
 // Every load is issued before the first store, so no wait for a load waits
 // on a store (loads and stores share one completion counter): the stores of
 // all four bands go out back to back behind one startup.
@@ -430,7 +430,7 @@ __global__ __launch_bounds__(512) void kband_kernel(const MmaArgs args, const Ep
             const v4_t v4 = *(const v4_t *)(stg + r * LD + col);
             const val_t v[4] = {v4[0], v4[1], v4[2], v4[3]};
             const int64_t grow = grow0 + i / RUNS;
-            if (grow < args.M && col < args.N) store4<E, val_t>(ep, zb, (int)grow, col, args.N, v);
+            if (grow < args.M && col < args.N) store4<E, val_t, StPol::NTWT>(ep, zb, (int)grow, col, args.N, v);
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);  // staging reads done before the next band's writes
         stage_barrier();

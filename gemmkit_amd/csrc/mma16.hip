@@ -364,6 +364,8 @@ void mma16_kernel(const MmaArgs args, const EpiParams ep) {
     // (unrolled under the unrolled block loop, 32 copies of it thrash the
     // instruction cache: requantized 4096^3 88 against 67 us).
     constexpr int IT_UNROLL = (E == EpiKind::Q8 || E == EpiKind::BF16) ? 1 : 16 / RPIT;
+    // i32 and requantized outputs are written through the L2 (StPol::WT).
+    constexpr StPol kPol = (E == EpiKind::I32 || E == EpiKind::Q8) ? StPol::WT : StPol::Plain;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -411,10 +413,10 @@ void mma16_kernel(const MmaArgs args, const EpiParams ep) {
                 // write stream; there the per-chunk address costs nothing
                 // measurable and they keep store4.
                 if (E == EpiKind::Q8 && ep.vec4 && gcol0 + c4 + 4 <= n_end)
-                    store4_at<E, val_t, false>(ep, cb + (int64_t)it * RPIT * row_step, v, s4, b4,
+                    store4_at<E, val_t, kPol>(ep, cb + (int64_t)it * RPIT * row_step, v, s4, b4,
                                                f4, tame);
                 else
-                    store4<E, val_t, false>(ep, z, grow, gcol0 + c4, n_end, v, s4, b4, f4);
+                    store4<E, val_t, kPol>(ep, z, grow, gcol0 + c4, n_end, v, s4, b4, f4);
             }
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);

@@ -921,7 +921,7 @@ void mma_kernel(const MmaArgs args, const EpiParams ep) {
                 }
             }
             if (lane_on && grow < args.M && gcol0 + c4 < n_end)
-                store4<E, val_t, false>(ep, z, grow, gcol0 + c4, n_end, v, s4, b4, f4);
+                store4<E, val_t, StPol::Plain>(ep, z, grow, gcol0 + c4, n_end, v, s4, b4, f4);
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_wave_barrier();
