@@ -154,19 +154,24 @@ struct Store<EpiKind::Q8> {
 //          data streams, such as the short-contraction kernel's rotating batches
 //          (the big tiles measured 1.7 us slower with it on 4096^3 i32 and 2 us on
 //          bf16 4096^3 with f32 out; the batched attention scores 4 us faster);
-//   WT     write-back with the sc1 (device scope) bit, which writes the line
-//          through the L2 as it is stored.  Same-process A/Bs on three boxes:
-//          the requantizing layer 2048x4096x11008 78.7 / 79.7 / 79.6 against
-//          80.7 / 81.8 / 81.7 us; int8 4096^3 with i32 out 56.2 / 58.8 / 58.3
-//          against 57.7 / 58.4 / 58.1 (box-dependent, kept for the same
-//          write pattern); f32 and bf16 outputs measured no change and keep
+//   WT     write-back with the sc1 (device scope) bit, which writes the data
+//          through the L2 as it is stored, in pieces per store instruction:
+//          right only where every instruction covers whole 128-byte lines.
+//          The big tile's i32 rows (256-byte segments) take it: int8 4096^3
+//          56.2 / 58.8 / 58.3 against 57.7 / 58.4 / 58.1 us in same-process
+//          A/Bs on three boxes, WRITE_SIZE unchanged.  The requantizing layer
+//          measured 2 us faster with it (78.7 / 79.7 / 79.6 against 80.7 /
+//          81.8 / 81.7) but its 176-byte row pieces then leave the L2 as
+//          partial lines, 27.0 MB written for the 22.5 MB output (1.2x), so it
+//          stays Plain; f32 and bf16 outputs measured no change and keep
 //          Plain / NT;
 //   NTWT   nontemporal with sc1: the band kernel's attention scores
 //          15.2-15.4 against 15.5-15.7 us with NT alone (four A/Bs).
 // Every policy stores the same bytes; only where the line is kept differs.
 enum class StPol { Plain, NT, WT, NTWT };
 
-// The requantized words follow WT and are stored Plain otherwise.
+// Requantized words follow a WT request and are stored Plain otherwise
+// (no kernel requests WT for them; see above).
 constexpr StPol q8_pol(StPol p) { return p == StPol::WT ? StPol::WT : StPol::Plain; }
 
 template <StPol P, typename V>

@@ -364,8 +364,9 @@ void mma16_kernel(const MmaArgs args, const EpiParams ep) {
     // (unrolled under the unrolled block loop, 32 copies of it thrash the
     // instruction cache: requantized 4096^3 88 against 67 us).
     constexpr int IT_UNROLL = (E == EpiKind::Q8 || E == EpiKind::BF16) ? 1 : 16 / RPIT;
-    // i32 and requantized outputs are written through the L2 (StPol::WT).
-    constexpr StPol kPol = (E == EpiKind::I32 || E == EpiKind::Q8) ? StPol::WT : StPol::Plain;
+    // i32 outputs are written through the L2 (StPol::WT; whole 16-byte
+    // chunks, 256 bytes per row segment, so whole lines go out).
+    constexpr StPol kPol = E == EpiKind::I32 ? StPol::WT : StPol::Plain;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll

@@ -327,9 +327,9 @@ void mma16w_kernel(const MmaArgs args, const EpiParams ep) {
             }
             if (grow < args.M && gcol < n_end) {
                 if (ep.vec4 && gcol + 4 <= n_end)
-                    store4_at<E, int32_t, StPol::WT>(ep, cb + off, v, s4, b4, nullptr, tame);
+                    store4_at<E, int32_t, StPol::Plain>(ep, cb + off, v, s4, b4, nullptr, tame);
                 else
-                    store4<E, int32_t, StPol::WT>(ep, z, grow, gcol, n_end, v, s4, b4, nullptr);
+                    store4<E, int32_t, StPol::Plain>(ep, z, grow, gcol, n_end, v, s4, b4, nullptr);
             }
             cc += STEP;
             row += 1;
