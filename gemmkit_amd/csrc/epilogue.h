@@ -163,8 +163,9 @@ struct Store<EpiKind::Q8> {
 //          measured 2 us faster with it (78.7 / 79.7 / 79.6 against 80.7 /
 //          81.8 / 81.7) but its 176-byte row pieces then leave the L2 as
 //          partial lines, 27.0 MB written for the 22.5 MB output (1.2x), so it
-//          stays Plain; f32 and bf16 outputs measured no change and keep
-//          Plain / NT;
+//          stays Plain.  f32 rows take it where the tile stores whole 1 KiB
+//          rows (0.5-0.6 us on bf16 4096^3 with f32 out); with the per-wave
+//          256-byte pieces f32 measured no change, bf16 output keeps NT;
 //   NTWT   nontemporal with sc1: the band kernel's attention scores
 //          15.2-15.4 against 15.5-15.7 us with NT alone (four A/Bs).
 // Every policy stores the same bytes; only where the line is kept differs.
