@@ -220,3 +220,46 @@ def test_i8_stepped_stores_16x16_tiles(dev, name, alpha, beta):
         gk.gemm_i8(alpha, gk.MatRef.from_row_major(to_dev(a, dev), m, k),
                    gk.MatRef(to_dev(b, dev), k, n, 1, k), beta, gk.MatMut(c, m, n, ldc, 1))
     assert np.array_equal(c.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("m,k,n,layout", [(333, 1024, 421, "row424"), (257, 512, 259, "row"),
+                                          (300, 640, 270, "col"), (256, 256, 256, "row")])
+def test_bf16_f32out_exact_16x16_tile(dev, m, k, n, layout):
+    """The 16x16-MFMA tile's f32 output (unfused: restaged as whole tile rows
+    and written through the L2) on integer-valued bf16 operands, where every
+    product, sum, alpha*acc + beta*C and the f32 result are exact: equal bit
+    for bit to the int64 product.  Covers a row stride that is a multiple of 4
+    with n not (whole chunks by vector, the last chunk element-wise), a row
+    stride that is not (element-wise), a column-major C (taken as the
+    transposed product) and a tile-aligned shape; the bytes around C stay."""
+    g = torch.Generator().manual_seed(0x7C1 + m)
+    ai = torch.randint(-8, 9, (m * k,), generator=g)
+    bi = torch.randint(-8, 9, (k * n,), generator=g)  # B column-major: (p, j) at j*k + p
+    c0 = torch.randint(-64, 65, (m * n,), generator=g).double() / 4
+    want = (0.75 * (ai.reshape(m, k).double() @ bi.reshape(n, k).double().T) +
+            0.5 * c0.reshape(m, n))  # |values| < 2^24 * 0.25: exact in f32
+    if layout == "col":
+        ld = m
+        cfull = torch.full((n * ld + 32,), -7.0, dtype=torch.float32)
+        cfull[:n * ld] = c0.reshape(m, n).T.contiguous().reshape(-1).float()
+        cm = lambda t: gk.MatMut(t, m, n, 1, ld)  # noqa: E731
+        got_of = lambda t: t[:n * ld].reshape(n, ld)[:, :m].T  # noqa: E731
+    else:
+        ld = 424 if layout == "row424" else n
+        cfull = torch.full((m * ld + 32,), -7.0, dtype=torch.float32)
+        cfull[:m * ld].reshape(m, ld)[:, :n] = c0.reshape(m, n).float()
+        cm = lambda t: gk.MatMut(t, m, n, ld, 1)  # noqa: E731
+        got_of = lambda t: t[:m * ld].reshape(m, ld)[:, :n]  # noqa: E731
+    c = cfull.to(dev)
+    a = ai.to(torch.bfloat16).to(dev)
+    b = bi.to(torch.bfloat16).to(dev)
+    with tile(M16):
+        gk.gemm_bf16_f32out(0.75, gk.MatRef.from_row_major(a, m, k), gk.MatRef(b, k, n, 1, k), 0.5,
+                            cm(c))
+    got = c.cpu()
+    assert torch.equal(got_of(got).double(), want), (m, k, n, layout)
+    # the padding and the tail past C keep their fill
+    if layout == "row424":
+        assert (got[:m * ld].reshape(m, ld)[:, n:] == -7.0).all()
+    tail = n * ld if layout == "col" else m * ld
+    assert (got[tail:] == -7.0).all()
