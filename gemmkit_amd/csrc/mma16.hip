@@ -388,8 +388,9 @@ void mma16_kernel(const MmaArgs args, const EpiParams ep) {
                                     (val_t)acc[i][j][3]};
                     *(v4_t *)(sb + l16 * LDW + wn * WTN + j * 16 + 4 * lq) = w;
                 }
-                // Every wave's block is staged, and (two blocks back) every
-                // wave's reads of this buffer are done.
+                // After this barrier every wave's block i is staged.  (The
+                // buffer was rewritten only after block i-1's barrier, which
+                // each wave reaches once its reads of block i-2 are done.)
                 __builtin_amdgcn_s_waitcnt(0xC07F);
                 stage_barrier();
                 const int grow0 = m0 + wm * WTM + i * 16 + wn * 4;
